@@ -1,0 +1,954 @@
+// emit_hip — lowers a validated program descriptor onto HIP kernels.
+//
+// The counterpart of the reference's Metal emitter (/root/reference/src/emit_metal.rs) and its
+// shared node→code recursion (/root/reference/src/codegen.rs:283-522), written for gfx950:
+//   * every fused stage is first offered to the hand-written CDNA4 skeletons (skeletons.cpp),
+//     which accept a stage from the structure of its carrier and leaves, never from a name;
+//   * otherwise it becomes the generic carrier fold: scalar (one lane per output point,
+//     emit_metal.rs:626-736), cooperative (a workgroup of wave64s folds one output point's
+//     stream and merges partial carriers with the carrier's own combine through DPP shuffles
+//     then LDS, emit_metal.rs:760-1101) or split (workgroups fold disjoint stream slices into a
+//     scratch arena and a second kernel merges them with the combine: the split-K combine,
+//     oracle interp.rs:555-643);
+//   * pointwise stages become one lane per output element, with the in-place `where` storing
+//     only where its condition holds (emit_metal.rs:1103-1178).
+// All arithmetic is f32 (accumulators included); loads widen from the storage dtype and the
+// single store narrows through it (emit_metal.rs:162-232).
+#include "emit.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <set>
+#include <sstream>
+
+namespace sanic {
+
+// ───────────────────────────── validation ─────────────────────────────────────────────────
+
+static int64_t vol(const int64_t* s, int r) {
+    int64_t v = 1;
+    for (int i = 0; i < r; i++) v *= s[i];
+    return v;
+}
+
+static std::vector<int64_t> shp(const sanic_node& n) { return {n.shape, n.shape + n.rank}; }
+
+int64_t dtype_bytes(int dt, int64_t n) {
+    switch (dt) {
+    case SANIC_F64: return 8 * n;
+    case SANIC_F32: case SANIC_U32: return 4 * n;
+    case SANIC_F16: case SANIC_BF16: return 2 * n;
+    case SANIC_I8: return n;
+    case SANIC_I4: case SANIC_U4: return (n + 1) / 2;
+    }
+    fail(SANIC_ERR_DTYPE, "unknown dtype " + std::to_string(dt));
+}
+
+static void check_node(const sanic_program_desc* d, int i) {
+    const sanic_node& n = d->nodes[i];
+    auto bad = [&](const std::string& m) {
+        fail(SANIC_ERR_COMPILE, "node " + std::to_string(i) + ": " + m);
+    };
+    if (n.rank < 0 || n.rank > SANIC_MAX_RANK) bad("rank out of range");
+    for (int k = 0; k < n.rank; k++)
+        if (n.shape[k] < 1) bad("non-positive extent");
+    for (int k = 0; k < n.n_in; k++)
+        if (n.in[k] < 0 || n.in[k] >= i) bad("child index must precede the node");
+    auto child = [&](int k) -> const sanic_node& { return d->nodes[n.in[k]]; };
+    switch (n.kind) {
+    case SANIC_NODE_INPUT: {
+        if (n.buffer < 0 || n.buffer >= d->n_buffers) bad("input buffer out of range");
+        const sanic_buffer_desc& b = d->buffers[n.buffer];
+        if (b.rank != n.rank || vol(b.shape, b.rank) != vol(n.shape, n.rank)) bad("input shape differs from its buffer");
+        for (int k = 0; k < n.rank; k++) if (b.shape[k] != n.shape[k]) bad("input shape differs from its buffer");
+        if (b.dtype != n.dtype) bad("input dtype differs from its buffer");
+        if (n.dtype == SANIC_F64) bad("f64 buffers are not a device storage format");
+        break;
+    }
+    case SANIC_NODE_CONST: if (n.rank != 0) bad("const must be rank 0"); break;
+    case SANIC_NODE_IOTA: if (n.rank != 1) bad("iota must be rank 1"); break;
+    case SANIC_NODE_COORDINATE: if (n.dim < 0 || n.dim >= n.rank) bad("coordinate dim"); break;
+    case SANIC_NODE_FOLD: break;
+    case SANIC_NODE_MAP: {
+        int ar = (n.op == SANIC_OP_WHERE) ? 3 : (n.op <= SANIC_OP_LT ? 2 : 1);
+        if (n.op < 0 || n.op > SANIC_OP_ROUND_F32 || n.n_in != ar) bad("map arity");
+        for (int k = 0; k < n.n_in; k++) {
+            const sanic_node& c = child(k);
+            if (c.rank > n.rank) bad("map input rank exceeds output rank");
+            int lead = n.rank - c.rank;
+            for (int j = 0; j < c.rank; j++)
+                if (c.shape[j] != 1 && c.shape[j] != n.shape[lead + j]) bad("map broadcast mismatch");
+        }
+        break;
+    }
+    case SANIC_NODE_REDUCE: {
+        const sanic_node& c = child(0);
+        if (n.n_in != 1 || n.dim < 0 || n.dim >= c.rank || n.rank != c.rank - 1) bad("reduce shape");
+        for (int j = 0, o = 0; j < c.rank; j++)
+            if (j != n.dim && c.shape[j] != n.shape[o++]) bad("reduce shape");
+        if (n.op < 0 || n.op > SANIC_MON_LSE) bad("reduce monoid");
+        break;
+    }
+    case SANIC_NODE_GATHER: {
+        const sanic_node& s = child(0);
+        const sanic_node& x = child(1);
+        if (n.n_in != 2 || n.dim < 0 || n.dim >= s.rank || n.rank != s.rank - 1 + x.rank) bad("gather shape");
+        for (int j = 0; j < n.rank; j++) {
+            int64_t want = j < n.dim ? s.shape[j] : j < n.dim + x.rank ? x.shape[j - n.dim] : s.shape[j - x.rank + 1];
+            if (n.shape[j] != want) bad("gather shape");
+        }
+        break;
+    }
+    case SANIC_NODE_VIEW: {
+        const sanic_node& s = child(0);
+        int sd = 0;
+        for (int j = 0; j < n.rank; j++) {
+            int g = n.group[j];
+            if (g < 1 || sd + g > s.rank) bad("view groups");
+            if (vol(s.shape + sd, g) != n.shape[j]) bad("view extent");
+            sd += g;
+        }
+        if (sd != s.rank) bad("view groups must cover the source");
+        break;
+    }
+    case SANIC_NODE_REINDEX: {
+        const sanic_node& s = child(0);
+        int64_t p = n.map_offset;
+        if (p < 0) bad("reindex map");
+        for (int j = 0; j < s.rank; j++) {
+            if (p + 2 > d->n_reindex) bad("reindex table overrun");
+            int64_t nt = d->reindex[p];
+            p += 2;
+            if (nt < 0 || p + 2 * nt > d->n_reindex) bad("reindex table overrun");
+            int64_t lo = d->reindex[p - 1], hi = lo;
+            for (int64_t t = 0; t < nt; t++) {
+                int64_t coef = d->reindex[p + 2 * t], od = d->reindex[p + 2 * t + 1];
+                if (od < 0 || od >= n.rank) bad("reindex output dim");
+                int64_t span = coef * (n.shape[od] - 1);
+                if (span < 0) lo += span; else hi += span;
+            }
+            p += 2 * nt;
+            if (!n.padded && (lo < 0 || hi >= s.shape[j])) bad("unpadded reindex reads out of bounds");
+        }
+        break;
+    }
+    default: bad("unknown node kind");
+    }
+}
+
+static void check_expr_tree(const sanic_program_desc* d, int root, int max_field, int allowed) {
+    if (root < 0 || root >= d->n_exprs) fail(SANIC_ERR_COMPILE, "expr root out of range");
+    std::vector<int> st{root};
+    while (!st.empty()) {
+        int i = st.back();
+        st.pop_back();
+        if (i < 0 || i >= d->n_exprs) fail(SANIC_ERR_COMPILE, "expr child out of range");
+        const sanic_expr& e = d->exprs[i];
+        if (e.op >= SANIC_EX_ITEM && e.op <= SANIC_EX_F) {
+            if (e.op != allowed && !(allowed == SANIC_EX_A && e.op == SANIC_EX_B))
+                fail(SANIC_ERR_COMPILE, "expr reads a field its context does not have");
+            if (e.index < 0 || e.index >= max_field) fail(SANIC_ERR_COMPILE, "expr field out of range");
+        } else if (e.op != SANIC_EX_CONST) {
+            if (e.op < 0 || e.op > SANIC_OP_ROUND_F32) fail(SANIC_ERR_COMPILE, "expr op");
+            for (int c : {e.a, e.b, e.c}) if (c >= 0) st.push_back(c);
+        }
+    }
+}
+
+static bool tree_has_fold(const sanic_program_desc* d, int root) {
+    const sanic_node& n = d->nodes[root];
+    if (n.kind == SANIC_NODE_FOLD) return true;
+    for (int k = 0; k < n.n_in; k++) if (tree_has_fold(d, n.in[k])) return true;
+    return false;
+}
+
+void validate(const sanic_program_desc* d) {
+    if (!d || d->n_nodes < 0 || d->n_stages < 1 || d->n_buffers < 1) fail(SANIC_ERR_ARG, "empty program");
+    for (int i = 0; i < d->n_nodes; i++) check_node(d, i);
+    for (int b = 0; b < d->n_buffers; b++) {
+        const sanic_buffer_desc& bd = d->buffers[b];
+        if (bd.rank < 0 || bd.rank > SANIC_MAX_RANK) fail(SANIC_ERR_COMPILE, "buffer rank");
+        if (bd.role < SANIC_BUF_INPUT || bd.role > SANIC_BUF_SCRATCH) fail(SANIC_ERR_COMPILE, "buffer role");
+        dtype_bytes(bd.dtype, 1);
+    }
+    for (int s = 0; s < d->n_stages; s++) {
+        const sanic_stage& st = d->stages[s];
+        auto bad = [&](const std::string& m) { fail(SANIC_ERR_COMPILE, "stage " + std::to_string(s) + ": " + m); };
+        if (st.out_buffer < 0 || st.out_buffer >= d->n_buffers) bad("output buffer");
+        const sanic_buffer_desc& ob = d->buffers[st.out_buffer];
+        if (ob.role == SANIC_BUF_INPUT) bad("a stage cannot write an input buffer");
+        if (ob.dtype != st.out_dtype) bad("output dtype differs from its buffer");
+        if (st.out_dtype == SANIC_F64 || st.out_dtype == SANIC_I4 || st.out_dtype == SANIC_U4 || st.out_dtype == SANIC_I8)
+            bad("unstorable output width (compile.rs:426-453)");
+        if (st.rank < 0 || st.rank > SANIC_MAX_RANK || vol(st.grid, st.rank) != vol(ob.shape, ob.rank)) bad("grid volume differs from the output buffer");
+        for (int k = 0; k < st.rank; k++) if (st.grid[k] < 1) bad("grid extent");
+        if (st.kind == SANIC_STAGE_FUSED) {
+            if (st.stream < 1) bad("empty stream");
+            if (st.n_leaves < 0 || st.n_leaves > SANIC_MAX_LEAVES) bad("leaf count");
+            for (int l = 0; l < st.n_leaves; l++) {
+                if (st.leaf[l] < 0 || st.leaf[l] >= d->n_nodes) bad("leaf node");
+                const sanic_node& ln = d->nodes[st.leaf[l]];
+                if (tree_has_fold(d, st.leaf[l])) bad("a leaf cannot read the fold value");
+                for (int j = 0; j < ln.rank; j++) {
+                    int b = st.bind[l][j];
+                    int64_t want = b == SANIC_BIND_STREAM ? st.stream : b == SANIC_BIND_BCAST ? 1 : (b >= 0 && b < st.rank ? st.grid[b] : -1);
+                    if (want != ln.shape[j]) bad("leaf " + std::to_string(l) + " dim " + std::to_string(j) + " binding mismatch");
+                }
+            }
+            const sanic_carrier& c = st.carrier;
+            if (c.slots < 1 || c.slots > SANIC_MAX_SLOTS) bad("slot count");
+            for (int k = 0; k < c.slots; k++) {
+                check_expr_tree(d, c.into[k], st.n_leaves, SANIC_EX_ITEM);
+                check_expr_tree(d, c.combine[k], c.slots, SANIC_EX_A);
+                const sanic_slot& sk = c.kind[k];
+                if ((sk.kind == SANIC_SLOT_EXP_SHIFTED || sk.kind == SANIC_SLOT_AT_EXTREMUM) &&
+                    (sk.ref_slot < 0 || sk.ref_slot >= c.slots)) bad("slot reference");
+            }
+            check_expr_tree(d, c.project, c.slots, SANIC_EX_F);
+            if (st.epilogue >= 0) {
+                if (st.epilogue >= d->n_nodes) bad("epilogue node");
+                const sanic_node& en = d->nodes[st.epilogue];
+                if (vol(en.shape, en.rank) != vol(st.grid, st.rank) || en.rank != st.rank) bad("epilogue shape");
+            }
+            for (int i = 0; i < d->n_nodes; i++)
+                if (d->nodes[i].kind == SANIC_NODE_FOLD && d->nodes[i].rank != st.rank && st.epilogue >= 0 && tree_has_fold(d, st.epilogue)) {}
+            if (st.sched.split < 0 || st.sched.waves < 0 || st.sched.chunk < 0) bad("fold schedule");
+        } else if (st.kind == SANIC_STAGE_POINTWISE) {
+            if (st.value < 0 || st.value >= d->n_nodes) bad("value node");
+            const sanic_node& vn = d->nodes[st.value];
+            if (vn.rank > st.rank) bad("value rank");
+            if (tree_has_fold(d, st.value)) bad("pointwise value reads a fold");
+            if (st.where >= 0 && st.where >= d->n_nodes) bad("where node");
+        } else {
+            bad("unknown stage kind");
+        }
+    }
+}
+
+// ───────────────────────────── rendering ──────────────────────────────────────────────────
+
+std::string flit(double v) {
+    if (std::isnan(v)) return "__builtin_nanf(\"\")";
+    if (std::isinf(v)) return v > 0 ? "__builtin_huge_valf()" : "(-__builtin_huge_valf())";
+    float f = (float)v;
+    if (std::isinf(f)) return f > 0 ? "__builtin_huge_valf()" : "(-__builtin_huge_valf())";
+    char buf[64];
+    snprintf(buf, sizeof buf, "%a", (double)f);
+    return std::string("((float)") + buf + ")";
+}
+
+const char* kPrelude = R"PRE(
+typedef long long idx_t;
+__device__ __forceinline__ float sanic_bf16(unsigned short b) { return __uint_as_float(((unsigned)b) << 16); }
+__device__ __forceinline__ unsigned short sanic_to_bf16(float v) {
+  unsigned b = __float_as_uint(v);
+  if (v != v) return (unsigned short)((b >> 16) | 0x0040u);
+  return (unsigned short)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float sanic_round_bf16(float v) { return sanic_bf16(sanic_to_bf16(v)); }
+__device__ __forceinline__ unsigned sanic_to_u32(float v) {
+  if (v >= 4294967040.0f) return 0xFFFFFFFFu;
+  if (!(v > 0.0f)) return 0u;
+  return (unsigned)(v + 0.5f);
+}
+__device__ __forceinline__ float sanic_w4(const unsigned char* p, idx_t i) {
+  return (float)(int)((p[i >> 1] >> ((i & 1) << 2)) & 0xF) - 8.0f;
+}
+__device__ __forceinline__ float sanic_u4(const unsigned char* p, idx_t i) {
+  return (float)(int)((p[i >> 1] >> ((i & 1) << 2)) & 0xF);
+}
+__device__ __forceinline__ float sanic_lse(float a, float b) {
+  if (a == -__builtin_huge_valf()) return b;
+  if (b == -__builtin_huge_valf()) return a;
+  float m = fmaxf(a, b);
+  return m + logf(expf(a - m) + expf(b - m));
+}
+)PRE";
+
+const char* ctype_of(int dt) {
+    switch (dt) {
+    case SANIC_F32: return "float";
+    case SANIC_F16: return "_Float16";
+    case SANIC_BF16: return "unsigned short";
+    case SANIC_U32: return "unsigned";
+    case SANIC_I8: return "signed char";
+    case SANIC_I4: case SANIC_U4: return "unsigned char";
+    }
+    return "float";
+}
+
+std::string map_expr(int op, const std::string& a, const std::string& b, const std::string& c) {
+    switch (op) {
+    case SANIC_OP_ADD: return "(" + a + " + " + b + ")";
+    case SANIC_OP_SUB: return "(" + a + " - " + b + ")";
+    case SANIC_OP_MUL: return "(" + a + " * " + b + ")";
+    case SANIC_OP_DIV: return "(" + a + " / " + b + ")";
+    case SANIC_OP_MAX: return "fmaxf(" + a + ", " + b + ")";
+    case SANIC_OP_MIN: return "fminf(" + a + ", " + b + ")";
+    case SANIC_OP_LT: return "((" + a + " < " + b + ") ? 1.0f : 0.0f)";
+    case SANIC_OP_NEG: return "(-" + a + ")";
+    case SANIC_OP_RECIP: return "(1.0f / " + a + ")";
+    case SANIC_OP_EXP: return "expf(" + a + ")";
+    case SANIC_OP_LOG: return "logf(" + a + ")";
+    case SANIC_OP_SQRT: return "sqrtf(" + a + ")";
+    case SANIC_OP_TANH: return "tanhf(" + a + ")";
+    case SANIC_OP_SIN: return "sinf(" + a + ")";
+    case SANIC_OP_COS: return "cosf(" + a + ")";
+    case SANIC_OP_WHERE: return "((" + a + " != 0.0f) ? " + b + " : " + c + ")";
+    case SANIC_OP_ROUND_BF16: return "sanic_round_bf16(" + a + ")";
+    case SANIC_OP_ROUND_F32: return "(" + a + ")";
+    }
+    fail(SANIC_ERR_COMPILE, "unknown map op");
+}
+
+std::string monoid_combine(int m, const std::string& a, const std::string& b) {
+    switch (m) {
+    case SANIC_MON_ADD: return "(" + a + " + " + b + ")";
+    case SANIC_MON_MUL: return "(" + a + " * " + b + ")";
+    case SANIC_MON_MAX: return "fmaxf(" + a + ", " + b + ")";
+    case SANIC_MON_MIN: return "fminf(" + a + ", " + b + ")";
+    case SANIC_MON_LSE: return "sanic_lse(" + a + ", " + b + ")";
+    }
+    fail(SANIC_ERR_COMPILE, "unknown monoid");
+}
+
+double monoid_identity(int m) {
+    switch (m) {
+    case SANIC_MON_ADD: return 0.0;
+    case SANIC_MON_MUL: return 1.0;
+    case SANIC_MON_MAX: case SANIC_MON_LSE: return -INFINITY;
+    default: return INFINITY;
+    }
+}
+
+std::string Code::str() const { return s.str(); }
+void Code::line(const std::string& l) {
+    for (int i = 0; i < indent; i++) s << "  ";
+    s << l << "\n";
+}
+
+std::string Renderer::param(int buffer) {
+    auto it = buf_param.find(buffer);
+    if (it != buf_param.end()) return it->second;
+    std::string name = "a.b" + std::to_string(buffer);
+    buf_param[buffer] = name;
+    bufs.push_back(buffer);
+    return name;
+}
+
+std::string Renderer::fresh(const char* p) { return std::string(p) + std::to_string(tmp++); }
+
+std::string Renderer::args_struct(const std::vector<std::string>& extra) const {
+    std::ostringstream o;
+    o << "struct Args {\n";
+    for (int b : bufs) {
+        int dt = d->buffers[b].dtype;
+        o << "  " << ctype_of(dt) << "* __restrict__ b" << b << ";\n";
+    }
+    for (auto& e : extra) o << "  " << e << ";\n";
+    o << "};\n";
+    return o.str();
+}
+
+std::vector<Arg> Renderer::arg_list() const {
+    std::vector<Arg> v;
+    for (int b : bufs) v.push_back({Arg::BUF, b});
+    return v;
+}
+
+std::string Renderer::load(int node, const std::vector<std::string>& c) {
+    const sanic_node& n = d->nodes[node];
+    std::string lin;
+    for (int j = 0; j < n.rank; j++) {
+        if (j == 0) lin = "(idx_t)(" + c[0] + ")";
+        else lin = "(" + lin + " * " + std::to_string(n.shape[j]) + " + (idx_t)(" + c[j] + "))";
+    }
+    if (lin.empty()) lin = "0";
+    std::string p = param(n.buffer);
+    switch (n.dtype) {
+    case SANIC_F32: return p + "[" + lin + "]";
+    case SANIC_F16: return "(float)" + p + "[" + lin + "]";
+    case SANIC_BF16: return "sanic_bf16(" + p + "[" + lin + "])";
+    case SANIC_U32: return "(float)" + p + "[" + lin + "]";
+    case SANIC_I8: return "(float)" + p + "[" + lin + "]";
+    case SANIC_I4: return "sanic_w4(" + p + ", " + lin + ")";
+    case SANIC_U4: return "sanic_u4(" + p + ", " + lin + ")";
+    }
+    fail(SANIC_ERR_DTYPE, "unloadable dtype");
+}
+
+// Emit the value of `node` at coordinates `c` (integer expressions) into `code`; returns an
+// expression (usually a fresh local) holding the f32 value.
+std::string Renderer::value(Code& code, int node, const std::vector<std::string>& c) {
+    const sanic_node& n = d->nodes[node];
+    std::string key = std::to_string(node) + "@";
+    for (auto& x : c) key += x + ",";
+    for (auto it = memo.rbegin(); it != memo.rend(); ++it) {
+        auto f = it->find(key);
+        if (f != it->end()) return f->second;
+    }
+    std::string out;
+    switch (n.kind) {
+    case SANIC_NODE_CONST: return flit(n.value);
+    case SANIC_NODE_IOTA: return "((float)(" + c[0] + "))";
+    case SANIC_NODE_COORDINATE: return "((float)(" + c[n.dim] + "))";
+    case SANIC_NODE_FOLD: return fold_var;
+    case SANIC_NODE_INPUT: {
+        out = fresh("v");
+        code.line("const float " + out + " = " + load(node, c) + ";");
+        break;
+    }
+    case SANIC_NODE_MAP: {
+        std::string a[3];
+        for (int k = 0; k < n.n_in; k++) {
+            const sanic_node& m = d->nodes[n.in[k]];
+            int lead = n.rank - m.rank;
+            std::vector<std::string> cc(m.rank);
+            for (int j = 0; j < m.rank; j++) cc[j] = m.shape[j] == 1 ? "0" : c[lead + j];
+            a[k] = value(code, n.in[k], cc);
+        }
+        out = fresh("m");
+        code.line("const float " + out + " = " + map_expr(n.op, a[0], a[1], a[2]) + ";");
+        break;
+    }
+    case SANIC_NODE_REDUCE: {
+        const sanic_node& m = d->nodes[n.in[0]];
+        out = fresh("r");
+        std::string r = fresh("i");
+        code.line("float " + out + " = " + flit(monoid_identity(n.op)) + ";");
+        code.line("for (idx_t " + r + " = 0; " + r + " < " + std::to_string(m.shape[n.dim]) + "; ++" + r + ") {");
+        code.indent++;
+        memo.emplace_back();
+        std::vector<std::string> cc;
+        for (int j = 0, o = 0; j < m.rank; j++) cc.push_back(j == n.dim ? r : c[o++]);
+        std::string v = value(code, n.in[0], cc);
+        code.line(out + " = " + monoid_combine(n.op, out, v) + ";");
+        memo.pop_back();
+        code.indent--;
+        code.line("}");
+        break;
+    }
+    case SANIC_NODE_GATHER: {
+        const sanic_node& s = d->nodes[n.in[0]];
+        const sanic_node& x = d->nodes[n.in[1]];
+        std::vector<std::string> ic(c.begin() + n.dim, c.begin() + n.dim + x.rank);
+        std::string iv = value(code, n.in[1], ic);
+        std::string gi = fresh("g");
+        // round half away from zero (f64::round), clamped so a bad index cannot fault
+        code.line("idx_t " + gi + " = (idx_t)roundf(" + iv + ");");
+        code.line(gi + " = " + gi + " < 0 ? 0 : (" + gi + " > " + std::to_string(s.shape[n.dim] - 1) + " ? " +
+                  std::to_string(s.shape[n.dim] - 1) + " : " + gi + ");");
+        std::vector<std::string> sc;
+        for (int j = 0; j < s.rank; j++)
+            sc.push_back(j < n.dim ? c[j] : j == n.dim ? gi : c[j - 1 + x.rank]);
+        return value(code, n.in[0], sc);
+    }
+    case SANIC_NODE_VIEW: {
+        const sanic_node& s = d->nodes[n.in[0]];
+        std::vector<std::string> sc(s.rank);
+        int sd = 0;
+        for (int j = 0; j < n.rank; j++) {
+            int g = n.group[j];
+            if (g == 1) { sc[sd] = c[j]; sd++; continue; }
+            int64_t inner = 1;
+            for (int t = g - 1; t >= 0; t--) {
+                int64_t ext = s.shape[sd + t];
+                std::string e = "((idx_t)(" + c[j] + ")";
+                if (inner != 1) e += " / " + std::to_string(inner);
+                e += ")";
+                if (t > 0) e = "(" + e + " % " + std::to_string(ext) + ")";
+                sc[sd + t] = e;
+                inner *= ext;
+            }
+            sd += g;
+        }
+        return value(code, n.in[0], sc);
+    }
+    case SANIC_NODE_REINDEX: {
+        const sanic_node& s = d->nodes[n.in[0]];
+        std::vector<std::string> sc(s.rank);
+        int64_t p = n.map_offset;
+        std::string ok;
+        for (int j = 0; j < s.rank; j++) {
+            int64_t nt = d->reindex[p], off = d->reindex[p + 1];
+            p += 2;
+            std::string e = std::to_string(off);
+            int64_t lo = off, hi = off;
+            for (int64_t t = 0; t < nt; t++) {
+                int64_t coef = d->reindex[p++], od = d->reindex[p++];
+                e += " + " + std::to_string(coef) + " * (idx_t)(" + c[od] + ")";
+                int64_t span = coef * (n.shape[od] - 1);
+                if (span < 0) lo += span; else hi += span;
+            }
+            std::string v = fresh("x");
+            code.line("const idx_t " + v + " = " + e + ";");
+            sc[j] = v;
+            if (n.padded && (lo < 0 || hi >= s.shape[j])) {
+                if (!ok.empty()) ok += " && ";
+                ok += "(" + v + " >= 0 && " + v + " < " + std::to_string(s.shape[j]) + ")";
+            }
+        }
+        if (ok.empty()) return value(code, n.in[0], sc);
+        out = fresh("p");
+        code.line("float " + out + " = 0.0f;");
+        code.line("if (" + ok + ") {");
+        code.indent++;
+        memo.emplace_back();
+        std::string v = value(code, n.in[0], sc);
+        code.line(out + " = " + v + ";");
+        memo.pop_back();
+        code.indent--;
+        code.line("}");
+        break;
+    }
+    default: fail(SANIC_ERR_COMPILE, "unrenderable node");
+    }
+    memo.back()[key] = out;
+    return out;
+}
+
+// Render a carrier Expr; fields map through `item`, `a`, `b`, `f` name prefixes.
+std::string Renderer::expr(Code& code, int e, const std::string& item, const std::string& a,
+                           const std::string& b, const std::string& f) {
+    const sanic_expr& x = d->exprs[e];
+    switch (x.op) {
+    case SANIC_EX_CONST: return flit(x.value);
+    case SANIC_EX_ITEM: return item + std::to_string(x.index);
+    case SANIC_EX_A: return a + std::to_string(x.index);
+    case SANIC_EX_B: return b + std::to_string(x.index);
+    case SANIC_EX_F: return f + std::to_string(x.index);
+    }
+    std::string s[3];
+    int kids[3] = {x.a, x.b, x.c};
+    for (int k = 0; k < 3; k++) if (kids[k] >= 0) s[k] = expr(code, kids[k], item, a, b, f);
+    std::string out = fresh("e");
+    code.line("const float " + out + " = " + map_expr(x.op, s[0], s[1], s[2]) + ";");
+    return out;
+}
+
+std::string store_stmt(const std::string& ptr, const std::string& idx, int dt, const std::string& v) {
+    switch (dt) {
+    case SANIC_F32: return ptr + "[" + idx + "] = " + v + ";";
+    case SANIC_F16: return ptr + "[" + idx + "] = (_Float16)" + v + ";";
+    case SANIC_BF16: return ptr + "[" + idx + "] = sanic_to_bf16(" + v + ");";
+    case SANIC_U32: return ptr + "[" + idx + "] = sanic_to_u32(" + v + ");";
+    }
+    fail(SANIC_ERR_DTYPE, "unstorable dtype");
+}
+
+void decode_grid(Code& code, const sanic_stage& st, const std::string& gid) {
+    std::string rem = gid;
+    for (int j = st.rank - 1; j >= 0; j--) {
+        if (j == 0) code.line("const idx_t g0 = " + rem + ";");
+        else {
+            code.line("const idx_t g" + std::to_string(j) + " = " + rem + " % " + std::to_string(st.grid[j]) + ";");
+            std::string nr = "q" + std::to_string(j);
+            code.line("const idx_t " + nr + " = " + rem + " / " + std::to_string(st.grid[j]) + ";");
+            rem = nr;
+        }
+    }
+}
+
+std::vector<std::string> leaf_coords(const sanic_stage& st, const sanic_program_desc* d, int l,
+                                     const std::string& s) {
+    const sanic_node& ln = d->nodes[st.leaf[l]];
+    std::vector<std::string> c(ln.rank);
+    for (int j = 0; j < ln.rank; j++) {
+        int b = st.bind[l][j];
+        c[j] = b == SANIC_BIND_STREAM ? s : b == SANIC_BIND_BCAST ? "0" : "g" + std::to_string(b);
+    }
+    return c;
+}
+
+// ───────────────────── honest window (emit_metal.rs:442-505, :555-585) ─────────────────────
+// A leaf that adds a prefix mask to the value feeding a Max slot lets the stream stop early:
+// masked elements contribute exactly nothing to the (m, ℓ, o) fold once one visible element
+// has been folded. Recognised forms (additive terms of the leaf, K ≤ −1e29 or −∞):
+//   where(E < s, K, 0)  → visible iff s ≤ E  → hi = floor(E) + 1
+//   where(s < E, 0, K)  → visible iff s < E  → hi = ceil(E)
+//   where(s < E, K, 0)  → visible iff s ≥ E  → lo = ceil(E)
+// where s is the stream coordinate and E does not depend on it.
+
+static bool depends_on_stream(const sanic_program_desc* d, int node, const std::vector<int>& bind_of_dims) {
+    // bind_of_dims: for the node's dims, which are the stream (value -1)
+    const sanic_node& n = d->nodes[node];
+    switch (n.kind) {
+    case SANIC_NODE_CONST: return false;
+    case SANIC_NODE_IOTA: return bind_of_dims[0] == SANIC_BIND_STREAM;
+    case SANIC_NODE_COORDINATE: return bind_of_dims[n.dim] == SANIC_BIND_STREAM;
+    case SANIC_NODE_MAP: {
+        for (int k = 0; k < n.n_in; k++) {
+            const sanic_node& m = d->nodes[n.in[k]];
+            int lead = n.rank - m.rank;
+            std::vector<int> b(m.rank);
+            for (int j = 0; j < m.rank; j++) b[j] = m.shape[j] == 1 ? SANIC_BIND_BCAST : bind_of_dims[lead + j];
+            if (depends_on_stream(d, n.in[k], b)) return true;
+        }
+        return false;
+    }
+    default: {
+        for (int j = 0; j < n.rank; j++) if (bind_of_dims[j] == SANIC_BIND_STREAM) return true;
+        return false;
+    }
+    }
+}
+
+static bool is_stream_coord(const sanic_program_desc* d, int node, const std::vector<int>& b) {
+    const sanic_node& n = d->nodes[node];
+    if (n.kind == SANIC_NODE_IOTA) return b[0] == SANIC_BIND_STREAM;
+    if (n.kind == SANIC_NODE_COORDINATE) return b[n.dim] == SANIC_BIND_STREAM;
+    return false;
+}
+
+static bool is_big_negative(const sanic_program_desc* d, int node) {
+    const sanic_node& n = d->nodes[node];
+    return n.kind == SANIC_NODE_CONST && n.value <= -1e29;
+}
+static bool is_zero(const sanic_program_desc* d, int node) {
+    const sanic_node& n = d->nodes[node];
+    return n.kind == SANIC_NODE_CONST && n.value == 0.0;
+}
+
+static std::vector<int> child_bind(const sanic_program_desc* d, int node, int k, const std::vector<int>& b) {
+    const sanic_node& n = d->nodes[node];
+    const sanic_node& m = d->nodes[n.in[k]];
+    int lead = n.rank - m.rank;
+    std::vector<int> cb(m.rank);
+    for (int j = 0; j < m.rank; j++) cb[j] = m.shape[j] == 1 ? SANIC_BIND_BCAST : b[lead + j];
+    return cb;
+}
+
+// Collect window bounds from additive mask terms of `node`.
+static void collect_window(const sanic_program_desc* d, int node, const std::vector<int>& b,
+                           std::vector<WindowBound>& out) {
+    const sanic_node& n = d->nodes[node];
+    if (n.kind != SANIC_NODE_MAP) return;
+    if (n.op == SANIC_OP_ADD) {
+        collect_window(d, n.in[0], child_bind(d, node, 0, b), out);
+        collect_window(d, n.in[1], child_bind(d, node, 1, b), out);
+        return;
+    }
+    if (n.op != SANIC_OP_WHERE) return;
+    const sanic_node& cond = d->nodes[n.in[0]];
+    if (cond.kind != SANIC_NODE_MAP || cond.op != SANIC_OP_LT) return;
+    std::vector<int> cb = child_bind(d, node, 0, b);
+    std::vector<int> lb = child_bind(d, n.in[0], 0, cb), rb = child_bind(d, n.in[0], 1, cb);
+    bool l_s = is_stream_coord(d, cond.in[0], lb), r_s = is_stream_coord(d, cond.in[1], rb);
+    bool l_dep = depends_on_stream(d, cond.in[0], lb), r_dep = depends_on_stream(d, cond.in[1], rb);
+    bool t_big = is_big_negative(d, n.in[1]), t_zero = is_zero(d, n.in[1]);
+    bool f_big = is_big_negative(d, n.in[2]), f_zero = is_zero(d, n.in[2]);
+    if (r_s && !l_dep && t_big && f_zero) out.push_back({WindowBound::HI_FLOOR_PLUS1, cond.in[0], lb});
+    else if (l_s && !r_dep && t_zero && f_big) out.push_back({WindowBound::HI_CEIL, cond.in[1], rb});
+    else if (l_s && !r_dep && t_big && f_zero) out.push_back({WindowBound::LO_CEIL, cond.in[1], rb});
+}
+
+// Window bounds for a fused stage: only when the carrier has an ExpShifted slot whose max slot's
+// `into` is exactly one item, and that item's leaf carries the mask terms.
+std::vector<WindowBound> honest_window(const sanic_program_desc* d, const sanic_stage& st) {
+    std::vector<WindowBound> out;
+    const sanic_carrier& c = st.carrier;
+    int max_slot = -1;
+    for (int k = 0; k < c.slots; k++)
+        if (c.kind[k].kind == SANIC_SLOT_EXP_SHIFTED) {
+            if (max_slot >= 0 && max_slot != c.kind[k].ref_slot) return out;
+            max_slot = c.kind[k].ref_slot;
+        }
+    if (max_slot < 0) return out;
+    if (c.kind[max_slot].kind != SANIC_SLOT_PLAIN || c.kind[max_slot].monoid != SANIC_MON_MAX) return out;
+    const sanic_expr& e = d->exprs[c.into[max_slot]];
+    if (e.op != SANIC_EX_ITEM) return out;
+    int l = e.index;
+    // the masked item may feed only the max slot's into (ExpShifted slots read it via the combine)
+    for (int k = 0; k < c.slots; k++) {
+        if (k == max_slot) continue;
+        std::vector<int> st_{c.into[k]};
+        while (!st_.empty()) {
+            int i = st_.back(); st_.pop_back();
+            const sanic_expr& x = d->exprs[i];
+            if (x.op == SANIC_EX_ITEM && x.index == l) return out;
+            for (int ch : {x.a, x.b, x.c}) if (ch >= 0 && x.op < SANIC_EX_CONST) st_.push_back(ch);
+        }
+    }
+    const sanic_node& ln = d->nodes[st.leaf[l]];
+    std::vector<int> b(st.bind[l], st.bind[l] + ln.rank);
+    collect_window(d, st.leaf[l], b, out);
+    return out;
+}
+
+void emit_window(Renderer& R, Code& code, const sanic_stage& st, const std::vector<WindowBound>& w,
+                 const std::string& lo, const std::string& hi) {
+    code.line("idx_t " + lo + " = 0, " + hi + " = " + std::to_string(st.stream) + ";");
+    for (auto& b : w) {
+        std::vector<std::string> c(b.bind.size());
+        for (size_t j = 0; j < b.bind.size(); j++)
+            c[j] = b.bind[j] == SANIC_BIND_BCAST ? "0" : b.bind[j] == SANIC_BIND_STREAM ? "0" : "g" + std::to_string(b.bind[j]);
+        std::string v = R.value(code, b.node, c);
+        switch (b.kind) {
+        case WindowBound::HI_FLOOR_PLUS1:
+            code.line("{ const float w_ = floorf(" + v + ") + 1.0f; if (w_ < (float)" + hi + ") " + hi + " = w_ < 0.0f ? 0 : (idx_t)w_; }");
+            break;
+        case WindowBound::HI_CEIL:
+            code.line("{ const float w_ = ceilf(" + v + "); if (w_ < (float)" + hi + ") " + hi + " = w_ < 0.0f ? 0 : (idx_t)w_; }");
+            break;
+        case WindowBound::LO_CEIL:
+            code.line("{ const float w_ = ceilf(" + v + "); if (w_ > (float)" + lo + ") " + lo + " = w_ > (float)" + std::to_string(st.stream) + " ? " + std::to_string(st.stream) + " : (idx_t)w_; }");
+            break;
+        }
+    }
+    // an empty visible range folds the whole stream, as the unmasked definition does
+    code.line("if (" + hi + " <= " + lo + ") { " + lo + " = 0; " + hi + " = " + std::to_string(st.stream) + "; }");
+}
+
+// ───────────────────────────── generic fold ───────────────────────────────────────────────
+
+static void emit_fold_body(Renderer& R, Code& code, const sanic_stage& st, const std::string& s) {
+    const sanic_carrier& c = st.carrier;
+    R.memo.emplace_back();
+    for (int l = 0; l < st.n_leaves; l++) {
+        std::string v = R.value(code, st.leaf[l], leaf_coords(st, R.d, l, s));
+        code.line("const float x" + std::to_string(l) + " = " + v + ";");
+    }
+    for (int k = 0; k < c.slots; k++) {
+        std::string v = R.expr(code, c.into[k], "x", "", "", "");
+        code.line("const float el" + std::to_string(k) + " = " + v + ";");
+    }
+    for (int k = 0; k < c.slots; k++) {
+        std::string v = R.expr(code, c.combine[k], "", "acc", "el", "");
+        code.line("const float nx" + std::to_string(k) + " = " + v + ";");
+    }
+    for (int k = 0; k < c.slots; k++) code.line("acc" + std::to_string(k) + " = nx" + std::to_string(k) + ";");
+    R.memo.pop_back();
+}
+
+// merge `acc` with `oth` (acc ⊕ oth) in place
+static void emit_merge(Renderer& R, Code& code, const sanic_carrier& c, const std::string& oth) {
+    code.line("{");
+    code.indent++;
+    for (int k = 0; k < c.slots; k++) {
+        std::string v = R.expr(code, c.combine[k], "", "acc", oth, "");
+        code.line("const float nx" + std::to_string(k) + " = " + v + ";");
+    }
+    for (int k = 0; k < c.slots; k++) code.line("acc" + std::to_string(k) + " = nx" + std::to_string(k) + ";");
+    code.indent--;
+    code.line("}");
+}
+
+static void emit_finish(Renderer& R, Code& code, const sanic_stage& st, const std::string& gid) {
+    std::string f = R.expr(code, st.carrier.project, "", "", "", "acc");
+    code.line("const float fold_v = " + f + ";");
+    std::string v = "fold_v";
+    if (st.epilogue >= 0) {
+        R.fold_var = "fold_v";
+        std::vector<std::string> gc;
+        for (int j = 0; j < st.rank; j++) gc.push_back("g" + std::to_string(j));
+        R.memo.emplace_back();
+        v = R.value(code, st.epilogue, gc);
+        R.memo.pop_back();
+    }
+    code.line(store_stmt(R.param(st.out_buffer), gid, st.out_dtype, v));
+}
+
+LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& scratch) {
+    const sanic_stage& st = d->stages[si];
+    const sanic_carrier& c = st.carrier;
+    LoweredStage L;
+    int64_t gvol = vol(st.grid, st.rank);
+    auto win = honest_window(d, st);
+    int split = st.sched.split > 1 ? (int)std::min<int64_t>(st.sched.split, st.stream) : 1;
+    int waves = st.sched.lane_stream ? std::max(1, std::min(16, st.sched.waves)) : 0;
+    int chunk = std::max(1, st.sched.chunk);
+    Renderer R(d);
+    Code body;
+    body.indent = 1;
+    std::ostringstream src;
+    src << kPrelude;
+
+    auto init_acc = [&](Code& code) {
+        for (int k = 0; k < c.slots; k++) code.line("float acc" + std::to_string(k) + " = " + flit(c.identity[k]) + ";");
+    };
+
+    if (waves == 0 && split == 1) {
+        L.kernel_kind = "fold:scalar";
+        body.line("const idx_t gid = (idx_t)blockIdx.x * 256 + threadIdx.x;");
+        body.line("if (gid >= " + std::to_string(gvol) + ") return;");
+        decode_grid(body, st, "gid");
+        init_acc(body);
+        emit_window(R, body, st, win, "lo", "hi");
+        body.line("for (idx_t s = lo; s < hi; ++s) {");
+        body.indent++;
+        emit_fold_body(R, body, st, "s");
+        body.indent--;
+        body.line("}");
+        emit_finish(R, body, st, "gid");
+        src << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(256) sanic_fold(Args a) {\n"
+            << body.str() << "}\n";
+        Launch ln{"sanic_fold", "", dim3((unsigned)((gvol + 255) / 256)), dim3(256), 0, R.arg_list()};
+        L.launches.push_back(ln);
+        L.source = src.str();
+        return L;
+    }
+
+    // cooperative / split: one workgroup of `nth` lanes folds one (grid point, split slice)
+    int nth = 64 * std::max(1, waves);
+    int nw = nth / 64;
+    L.kernel_kind = split > 1 ? "fold:split" : "fold:coop";
+    int64_t part_off = scratch;
+    if (split > 1) scratch += ((gvol * split * c.slots * 4 + 255) / 256) * 256;
+    body.line("const idx_t gid = (idx_t)blockIdx.x / " + std::to_string(split) + ";");
+    body.line("const int part = (int)(blockIdx.x % " + std::to_string(split) + ");");
+    body.line("const int t = threadIdx.x, lane = t & 63, wv = t >> 6;");
+    decode_grid(body, st, "gid");
+    init_acc(body);
+    emit_window(R, body, st, win, "lo0", "hi0");
+    body.line("const idx_t span_ = hi0 - lo0;");
+    body.line("const idx_t lo = lo0 + (idx_t)part * span_ / " + std::to_string(split) + ";");
+    body.line("const idx_t hi = lo0 + ((idx_t)part + 1) * span_ / " + std::to_string(split) + ";");
+    body.line("for (idx_t base = lo + (idx_t)t * " + std::to_string(chunk) + "; base < hi; base += " +
+              std::to_string((int64_t)nth * chunk) + ") {");
+    body.indent++;
+    body.line("#pragma unroll");
+    body.line("for (int j = 0; j < " + std::to_string(chunk) + "; ++j) {");
+    body.indent++;
+    body.line("const idx_t s = base + j;");
+    body.line("if (s < hi) {");
+    body.indent++;
+    emit_fold_body(R, body, st, "s");
+    body.indent--;
+    body.line("}");
+    body.indent--;
+    body.line("}");
+    body.indent--;
+    body.line("}");
+    // wave-level butterfly: the lower lane's partial is the left operand, so the merge order
+    // follows lane order
+    body.line("for (int off = 1; off < 64; off <<= 1) {");
+    body.indent++;
+    for (int k = 0; k < c.slots; k++)
+        body.line("float o" + std::to_string(k) + " = __shfl_xor(acc" + std::to_string(k) + ", off, 64);");
+    body.line("if (lane & off) {");
+    body.indent++;
+    for (int k = 0; k < c.slots; k++)
+        body.line("const float sw" + std::to_string(k) + " = acc" + std::to_string(k) + "; acc" + std::to_string(k) + " = o" +
+                  std::to_string(k) + "; o" + std::to_string(k) + " = sw" + std::to_string(k) + ";");
+    body.indent--;
+    body.line("}");
+    emit_merge(R, body, c, "o");
+    body.indent--;
+    body.line("}");
+    if (nw > 1) {
+        body.line("__shared__ float lds_acc[" + std::to_string(nw) + "][" + std::to_string(c.slots) + "];");
+        body.line("if (lane == 0) {");
+        for (int k = 0; k < c.slots; k++) body.line("  lds_acc[wv][" + std::to_string(k) + "] = acc" + std::to_string(k) + ";");
+        body.line("}");
+        body.line("__syncthreads();");
+        body.line("if (t != 0) return;");
+        body.line("for (int w = 1; w < " + std::to_string(nw) + "; ++w) {");
+        body.indent++;
+        for (int k = 0; k < c.slots; k++)
+            body.line("const float o" + std::to_string(k) + " = lds_acc[w][" + std::to_string(k) + "];");
+        emit_merge(R, body, c, "o");
+        body.indent--;
+        body.line("}");
+    } else {
+        body.line("if (t != 0) return;");
+    }
+    if (split == 1) {
+        emit_finish(R, body, st, "gid");
+        src << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(" << nth
+            << ") sanic_fold(Args a) {\n" << body.str() << "}\n";
+        Launch ln{"sanic_fold", "", dim3((unsigned)gvol), dim3(nth), 0, R.arg_list()};
+        L.launches.push_back(ln);
+        L.source = src.str();
+        return L;
+    }
+    // split: write the partial carrier, then a second kernel merges with the combine
+    for (int k = 0; k < c.slots; k++)
+        body.line("a.scratch[((idx_t)gid * " + std::to_string(split) + " + part) * " + std::to_string(c.slots) + " + " +
+                  std::to_string(k) + "] = acc" + std::to_string(k) + ";");
+    Code mb;
+    mb.indent = 1;
+    Renderer R2(d);
+    R2.bufs = R.bufs;
+    R2.buf_param = R.buf_param;
+    mb.line("const idx_t gid = (idx_t)blockIdx.x * 256 + threadIdx.x;");
+    mb.line("if (gid >= " + std::to_string(gvol) + ") return;");
+    decode_grid(mb, st, "gid");
+    mb.line("const float* pp = a.scratch + (idx_t)gid * " + std::to_string(split * c.slots) + ";");
+    for (int k = 0; k < c.slots; k++) mb.line("float acc" + std::to_string(k) + " = pp[" + std::to_string(k) + "];");
+    mb.line("for (int p = 1; p < " + std::to_string(split) + "; ++p) {");
+    mb.indent++;
+    for (int k = 0; k < c.slots; k++)
+        mb.line("const float o" + std::to_string(k) + " = pp[p * " + std::to_string(c.slots) + " + " + std::to_string(k) + "];");
+    emit_merge(R2, mb, c, "o");
+    mb.indent--;
+    mb.line("}");
+    emit_finish(R2, mb, st, "gid");
+    // both kernels share one Args layout: the union of their buffers
+    for (int b : R2.bufs) R.param(b);
+    src << R.args_struct({"float* __restrict__ scratch"});
+    src << "extern \"C\" __global__ void __launch_bounds__(" << nth << ") sanic_fold_part(Args a) {\n" << body.str() << "}\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) sanic_fold_merge(Args a) {\n" << mb.str() << "}\n";
+    std::vector<Arg> args = R.arg_list();
+    args.push_back({Arg::SCRATCH, part_off});
+    L.launches.push_back({"sanic_fold_part", "", dim3((unsigned)(gvol * split)), dim3(nth), 0, args});
+    L.launches.push_back({"sanic_fold_merge", "", dim3((unsigned)((gvol + 255) / 256)), dim3(256), 0, args});
+    L.source = src.str();
+    return L;
+}
+
+LoweredStage lower_pointwise(const sanic_program_desc* d, int si) {
+    const sanic_stage& st = d->stages[si];
+    LoweredStage L;
+    L.kernel_kind = st.where >= 0 ? "pointwise:in-place-where" : "pointwise";
+    Renderer R(d);
+    Code body;
+    body.indent = 1;
+    int64_t gvol = vol(st.grid, st.rank);
+    body.line("const idx_t gid = (idx_t)blockIdx.x * 256 + threadIdx.x;");
+    body.line("if (gid >= " + std::to_string(gvol) + ") return;");
+    decode_grid(body, st, "gid");
+    std::vector<std::string> gc;
+    for (int j = 0; j < st.rank; j++) gc.push_back("g" + std::to_string(j));
+    auto at = [&](int node) {
+        const sanic_node& n = d->nodes[node];
+        int lead = st.rank - n.rank;
+        std::vector<std::string> c(n.rank);
+        for (int j = 0; j < n.rank; j++) c[j] = n.shape[j] == 1 ? "0" : gc[lead + j];
+        return R.value(body, node, c);
+    };
+    if (st.where >= 0) {
+        std::string w = at(st.where);
+        body.line("if (" + w + " == 0.0f) return;");
+    }
+    std::string v = at(st.value);
+    body.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v));
+    std::ostringstream src;
+    src << kPrelude << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(256) sanic_pointwise(Args a) {\n"
+        << body.str() << "}\n";
+    L.source = src.str();
+    L.launches.push_back({"sanic_pointwise", "", dim3((unsigned)((gvol + 255) / 256)), dim3(256), 0, R.arg_list()});
+    return L;
+}
+
+Lowered lower_program(const sanic_program_desc* d) {
+    validate(d);
+    Lowered out;
+    for (int s = 0; s < d->n_stages; s++) {
+        const sanic_stage& st = d->stages[s];
+        LoweredStage L;
+        bool done = false;
+        if (st.kind == SANIC_STAGE_FUSED) {
+            done = lower_skeleton(d, s, out.scratch_bytes, L);
+            if (!done) L = lower_generic_fold(d, s, out.scratch_bytes);
+        } else {
+            done = lower_pointwise_skeleton(d, s, out.scratch_bytes, L);
+            if (!done) L = lower_pointwise(d, s);
+        }
+        out.stages.push_back(std::move(L));
+    }
+    return out;
+}
+
+}  // namespace sanic

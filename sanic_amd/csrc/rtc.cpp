@@ -1,0 +1,89 @@
+// hipRTC compilation of generated kernels, with an on-disk code-object cache keyed by a hash of
+// the source and the options (the reference compiles MSL at runtime, metal.rs:166-185; this is
+// its counterpart). No fast-math: ±inf and NaN semantics are kept, as the reference does for
+// the −∞ mask (tests/reserved_cache.rs:1-12).
+#include <hip/hiprtc.h>
+
+#include <dlfcn.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cstring>
+#include <fstream>
+#include <mutex>
+#include <sstream>
+
+#include "common.h"
+
+namespace sanic {
+
+static const char* kOptions[] = {
+    "--offload-arch=gfx950", "-O3", "-std=c++17",
+    // packed-f32 instruction forms are disabled: some have returned wrong results on MI355X
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+};
+
+static uint64_t fnv1a(const std::string& s, uint64_t h = 1469598103934665603ULL) {
+    for (unsigned char c : s) { h ^= c; h *= 1099511628211ULL; }
+    return h;
+}
+
+static std::string cache_dir() {
+    if (const char* e = getenv("SANIC_HIP_CACHE")) return e;
+    Dl_info info;
+    if (dladdr((void*)&cache_dir, &info) && info.dli_fname) {
+        std::string p = info.dli_fname;
+        auto slash = p.rfind('/');
+        if (slash != std::string::npos) return p.substr(0, slash) + "/_kcache";
+    }
+    return "/tmp/sanic_hip_kcache";
+}
+
+static bool read_file(const std::string& path, std::string& out) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) return false;
+    std::stringstream ss;
+    ss << f.rdbuf();
+    out = ss.str();
+    return !out.empty();
+}
+
+std::string compile_source(const std::string& source) {
+    std::string opts_key;
+    for (auto* o : kOptions) opts_key += o, opts_key += ' ';
+    char hex[32];
+    snprintf(hex, sizeof hex, "%016llx", (unsigned long long)fnv1a(opts_key + source));
+    std::string dir = cache_dir();
+    std::string path = dir + "/" + hex + ".co";
+    std::string code;
+    if (!getenv("SANIC_HIP_NO_CACHE") && read_file(path, code)) return code;
+
+    hiprtcProgram prog;
+    if (hiprtcCreateProgram(&prog, source.c_str(), "sanic_kernel.hip", 0, nullptr, nullptr) !=
+        HIPRTC_SUCCESS)
+        fail(SANIC_ERR_COMPILE, "hiprtcCreateProgram failed");
+    hiprtcResult r = hiprtcCompileProgram(prog, (int)(sizeof kOptions / sizeof *kOptions), kOptions);
+    if (r != HIPRTC_SUCCESS) {
+        size_t n = 0;
+        hiprtcGetProgramLogSize(prog, &n);
+        std::string log(n + 1, '\0');
+        hiprtcGetProgramLog(prog, log.data());
+        hiprtcDestroyProgram(&prog);
+        fail(SANIC_ERR_COMPILE, "hipRTC compile failed:\n" + log + "\n--- source ---\n" + source);
+    }
+    size_t n = 0;
+    hiprtcGetCodeSize(prog, &n);
+    code.resize(n);
+    hiprtcGetCode(prog, code.data());
+    hiprtcDestroyProgram(&prog);
+    mkdir(dir.c_str(), 0755);
+    std::string tmp = path + ".tmp." + std::to_string(getpid());
+    {
+        std::ofstream f(tmp, std::ios::binary);
+        f.write(code.data(), (std::streamsize)code.size());
+    }
+    rename(tmp.c_str(), path.c_str());
+    return code;
+}
+
+}  // namespace sanic

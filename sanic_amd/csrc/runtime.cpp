@@ -1,0 +1,573 @@
+// The HIP runtime behind the C ABI: device, buffers, prepared executables, eager execution and
+// hipGraph capture/replay.
+//
+// Counterparts in the reference: MetalDevice (/root/reference/src/metal.rs:148-838), the Metal
+// Backend impl (/root/reference/src/compile.rs:694-787) and MetalReplay
+// (/root/reference/src/compile.rs:800-1035). One HIP stream per device serialises the stages,
+// so the reference's static barrier schedule (metal.rs:754-796) is implied by stream order; a
+// replay is one hipGraph whose kernel nodes follow that order.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <thread>
+
+#include "emit.h"
+
+namespace sanic {
+
+static thread_local std::string g_last_error;
+void set_last_error(const std::string& s) { g_last_error = s; }
+
+}  // namespace sanic
+
+using namespace sanic;
+
+struct sanic_hip_device {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    hipDeviceProp_t props{};
+};
+
+struct Storage {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    bool owned = false;
+    int ordinal = 0;
+    ~Storage() {
+        if (owned && ptr) {
+            hipSetDevice(ordinal);
+            hipFree(ptr);
+        }
+    }
+};
+
+struct sanic_hip_buffer {
+    sanic_hip_device* dev = nullptr;
+    std::shared_ptr<Storage> storage;
+    size_t offset = 0;
+    size_t bytes = 0;
+    char* ptr() const { return (char*)storage->ptr + offset; }
+};
+
+struct Module {
+    hipModule_t mod = nullptr;
+};
+
+struct sanic_hip_exe {
+    sanic_hip_device* dev = nullptr;
+    std::vector<sanic_buffer_desc> buffers;
+    std::vector<int> stage_out;       // output buffer of each stage
+    std::vector<int> stage_out_role;
+    Lowered low;
+    std::map<std::string, std::shared_ptr<Module>> modules;  // source -> module
+    ~sanic_hip_exe() {
+        for (auto& kv : modules)
+            if (kv.second->mod) hipModuleUnload(kv.second->mod);
+    }
+};
+
+struct sanic_hip_replay {
+    sanic_hip_exe* exe = nullptr;
+    std::vector<sanic_hip_buffer*> bound;     // per program buffer (borrowed or owned)
+    std::vector<std::unique_ptr<sanic_hip_buffer>> owned;
+    std::unique_ptr<sanic_hip_buffer> scratch;
+    std::vector<std::pair<int, int>> feedback;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    ~sanic_hip_replay() {
+        if (graph_exec) hipGraphExecDestroy(graph_exec);
+        if (graph) hipGraphDestroy(graph);
+        if (ev0) hipEventDestroy(ev0);
+        if (ev1) hipEventDestroy(ev1);
+    }
+};
+
+// ── built-in kernels: scratch clearing (graph-safe, no memset nodes) and feedback conversion ──
+
+__global__ void sanic_zero_words(uint32_t* p, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+__device__ float load_as_float(const void* p, int dt, int64_t i) {
+    switch (dt) {
+    case SANIC_F32: return ((const float*)p)[i];
+    case SANIC_BF16: return __uint_as_float(((uint32_t)((const uint16_t*)p)[i]) << 16);
+    case SANIC_U32: return (float)((const uint32_t*)p)[i];
+    case SANIC_F16: return (float)((const _Float16*)p)[i];
+    default: return 0.0f;
+    }
+}
+
+__device__ void store_from_float(void* p, int dt, int64_t i, float v) {
+    switch (dt) {
+    case SANIC_F32: ((float*)p)[i] = v; break;
+    case SANIC_BF16: {
+        uint32_t b = __float_as_uint(v);
+        uint16_t r = (v != v) ? (uint16_t)((b >> 16) | 0x40u) : (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+        ((uint16_t*)p)[i] = r;
+        break;
+    }
+    case SANIC_U32: ((uint32_t*)p)[i] = v >= 4294967040.0f ? 0xFFFFFFFFu : (!(v > 0.0f) ? 0u : (uint32_t)(v + 0.5f)); break;
+    case SANIC_F16: ((_Float16*)p)[i] = (_Float16)v; break;
+    default: break;
+    }
+}
+
+__global__ void sanic_convert(const void* src, int sdt, void* dst, int ddt, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) store_from_float(dst, ddt, i, load_as_float(src, sdt, i));
+}
+
+// ── helpers ──────────────────────────────────────────────────────────────────────────────
+
+template <class F>
+static int guarded(F&& f) {
+    try {
+        f();
+        return SANIC_OK;
+    } catch (const Error& e) {
+        set_last_error(e.what());
+        return e.code;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return SANIC_ERR_BACKEND;
+    }
+}
+
+static int64_t buffer_bytes(const sanic_buffer_desc& b) {
+    int64_t n = 1;
+    for (int i = 0; i < b.rank; i++) n *= b.shape[i];
+    return dtype_bytes(b.dtype, n);
+}
+
+static sanic_hip_buffer* new_buffer(sanic_hip_device* dev, size_t bytes) {
+    SANIC_HIP(hipSetDevice(dev->ordinal));
+    auto st = std::make_shared<Storage>();
+    st->bytes = bytes;
+    st->owned = true;
+    st->ordinal = dev->ordinal;
+    SANIC_HIP(hipMalloc(&st->ptr, std::max<size_t>(bytes, 256)));
+    auto* b = new sanic_hip_buffer;
+    b->dev = dev;
+    b->storage = st;
+    b->bytes = bytes;
+    return b;
+}
+
+static void compile_all(sanic_hip_exe* exe, bool load) {
+    std::vector<std::string> sources;
+    for (auto& s : exe->low.stages)
+        if (!exe->modules.count(s.source)) {
+            exe->modules[s.source] = std::make_shared<Module>();
+            sources.push_back(s.source);
+        }
+    std::vector<std::string> codes(sources.size());
+    std::vector<std::string> errors(sources.size());
+    std::vector<int> err_codes(sources.size(), 0);
+    std::atomic<size_t> next{0};
+    int nthreads = (int)std::min<size_t>(sources.size(), std::max(1u, std::min(16u, std::thread::hardware_concurrency())));
+    std::vector<std::thread> pool;
+    for (int t = 0; t < nthreads; t++)
+        pool.emplace_back([&] {
+            for (size_t i = next++; i < sources.size(); i = next++) {
+                try {
+                    codes[i] = compile_source(sources[i]);
+                } catch (const Error& e) {
+                    errors[i] = e.what();
+                    err_codes[i] = e.code;
+                }
+            }
+        });
+    for (auto& th : pool) th.join();
+    for (size_t i = 0; i < sources.size(); i++)
+        if (err_codes[i]) fail(err_codes[i], errors[i]);
+    if (!load) return;
+    for (size_t i = 0; i < sources.size(); i++)
+        SANIC_HIP(hipModuleLoadData(&exe->modules[sources[i]]->mod, codes[i].data()));
+    for (auto& s : exe->low.stages)
+        for (auto& l : s.launches)
+            SANIC_HIP(hipModuleGetFunction(&l.fn, exe->modules[s.source]->mod, l.kernel.c_str()));
+}
+
+// Enqueue every stage's launches on the device stream. `bound[i]` is program buffer i.
+static void enqueue(sanic_hip_exe* exe, const std::vector<sanic_hip_buffer*>& bound, char* scratch,
+                    hipEvent_t* stage_events = nullptr) {
+    hipStream_t s = exe->dev->stream;
+    for (size_t si = 0; si < exe->low.stages.size(); si++) {
+        if (stage_events) SANIC_HIP(hipEventRecord(stage_events[si], s));
+        for (auto& l : exe->low.stages[si].launches) {
+            if (l.zero_scratch && l.zero_bytes > 0) {
+                int64_t words = l.zero_bytes / 4;
+                unsigned blocks = (unsigned)std::min<int64_t>((words + 255) / 256, 4096);
+                hipLaunchKernelGGL(sanic_zero_words, dim3(blocks), dim3(256), 0, s, (uint32_t*)(scratch + l.zero_off), words);
+                SANIC_HIP(hipGetLastError());
+            }
+            std::vector<uint64_t> kargs;
+            for (auto& a : l.args) {
+                switch (a.kind) {
+                case Arg::BUF: {
+                    sanic_hip_buffer* b = bound[a.v];
+                    if (!b) fail(SANIC_ERR_MISSING_INPUT, "buffer " + std::to_string(a.v) + " is not bound");
+                    kargs.push_back((uint64_t)(uintptr_t)b->ptr());
+                    break;
+                }
+                case Arg::SCRATCH: kargs.push_back((uint64_t)(uintptr_t)(scratch + a.v)); break;
+                case Arg::IMM: kargs.push_back((uint64_t)a.v); break;
+                }
+            }
+            size_t sz = kargs.size() * 8;
+            void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, kargs.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+                           HIP_LAUNCH_PARAM_END};
+            SANIC_HIP(hipModuleLaunchKernel(l.fn, l.grid.x, l.grid.y, l.grid.z, l.block.x, l.block.y, l.block.z,
+                                            l.lds, s, nullptr, cfg));
+        }
+    }
+    if (stage_events) SANIC_HIP(hipEventRecord(stage_events[exe->low.stages.size()], s));
+}
+
+static void check_binding(sanic_hip_exe* exe, int i, sanic_hip_buffer* b) {
+    const sanic_buffer_desc& bd = exe->buffers[i];
+    if (!b) fail(SANIC_ERR_MISSING_INPUT, "program buffer " + std::to_string(i) + " is not bound (MissingInput)");
+    if ((int64_t)b->bytes < buffer_bytes(bd))
+        fail(SANIC_ERR_SHAPE, "program buffer " + std::to_string(i) + " binding holds " + std::to_string(b->bytes) +
+                                  " bytes; its shape needs " + std::to_string(buffer_bytes(bd)));
+    if (b->dev != exe->dev) fail(SANIC_ERR_ARG, "binding lives on another device");
+}
+
+// ── C ABI ────────────────────────────────────────────────────────────────────────────────
+
+extern "C" {
+
+const char* sanic_hip_last_error(void) { return g_last_error.c_str(); }
+
+int sanic_hip_open(int ordinal, sanic_hip_device** out) {
+    return guarded([&] {
+        if (!out) fail(SANIC_ERR_ARG, "null out");
+        *out = nullptr;
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess || n <= ordinal || ordinal < 0)
+            fail(SANIC_ERR_BACKEND, "no HIP device " + std::to_string(ordinal));
+        auto* d = new sanic_hip_device;
+        d->ordinal = ordinal;
+        SANIC_HIP(hipSetDevice(ordinal));
+        SANIC_HIP(hipGetDeviceProperties(&d->props, ordinal));
+        SANIC_HIP(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+        *out = d;
+    });
+}
+
+void sanic_hip_close(sanic_hip_device* dev) {
+    if (!dev) return;
+    hipSetDevice(dev->ordinal);
+    if (dev->stream) {
+        hipStreamSynchronize(dev->stream);
+        hipStreamDestroy(dev->stream);
+    }
+    delete dev;
+}
+
+int sanic_hip_specs(sanic_hip_device* dev, sanic_device_specs* out) {
+    return guarded([&] {
+        if (!dev || !out) fail(SANIC_ERR_ARG, "null argument");
+        memset(out, 0, sizeof *out);
+        snprintf(out->name, sizeof out->name, "%s", dev->props.gcnArchName);
+        out->compute_units = dev->props.multiProcessorCount;
+        out->wave_size = dev->props.warpSize;
+        out->lds_bytes_per_cu = 160 * 1024;
+        out->hbm_bytes_per_s = 8.0e12;             // MI355X HBM3E
+        out->bf16_mfma_flops = 2.5e15;             // dense bf16 MFMA
+        out->f32_flops = 157.3e12;
+        out->clock_hz = dev->props.clockRate * 1000.0;
+        out->hbm_bytes = (int64_t)dev->props.totalGlobalMem;
+    });
+}
+
+int sanic_hip_alloc(sanic_hip_device* dev, size_t bytes, sanic_hip_buffer** out) {
+    return guarded([&] {
+        if (!dev || !out) fail(SANIC_ERR_ARG, "null argument");
+        *out = new_buffer(dev, bytes);
+    });
+}
+
+void sanic_hip_free(sanic_hip_buffer* buf) { delete buf; }
+
+int sanic_hip_upload(sanic_hip_buffer* buf, size_t offset, const void* host, size_t bytes) {
+    return guarded([&] {
+        if (!buf || (!host && bytes)) fail(SANIC_ERR_ARG, "null argument");
+        if (offset + bytes > buf->bytes) fail(SANIC_ERR_ARG, "upload past the end of the buffer");
+        SANIC_HIP(hipSetDevice(buf->dev->ordinal));
+        SANIC_HIP(hipMemcpyAsync(buf->ptr() + offset, host, bytes, hipMemcpyHostToDevice, buf->dev->stream));
+        SANIC_HIP(hipStreamSynchronize(buf->dev->stream));
+    });
+}
+
+int sanic_hip_download(sanic_hip_buffer* buf, size_t offset, void* host, size_t bytes) {
+    return guarded([&] {
+        if (!buf || (!host && bytes)) fail(SANIC_ERR_ARG, "null argument");
+        if (offset + bytes > buf->bytes) fail(SANIC_ERR_ARG, "download past the end of the buffer");
+        SANIC_HIP(hipSetDevice(buf->dev->ordinal));
+        SANIC_HIP(hipMemcpyAsync(host, buf->ptr() + offset, bytes, hipMemcpyDeviceToHost, buf->dev->stream));
+        SANIC_HIP(hipStreamSynchronize(buf->dev->stream));
+    });
+}
+
+int sanic_hip_slice(sanic_hip_buffer* buf, size_t offset, size_t bytes, sanic_hip_buffer** out) {
+    return guarded([&] {
+        if (!buf || !out) fail(SANIC_ERR_ARG, "null argument");
+        if (offset % 4) fail(SANIC_ERR_ARG, "slice offsets must be 4-byte aligned (metal.rs:80-90)");
+        if (offset + bytes > buf->bytes) fail(SANIC_ERR_ARG, "slice past the end of the buffer");
+        auto* b = new sanic_hip_buffer(*buf);
+        b->offset = buf->offset + offset;
+        b->bytes = bytes;
+        *out = b;
+    });
+}
+
+size_t sanic_hip_buffer_bytes(const sanic_hip_buffer* buf) { return buf ? buf->bytes : 0; }
+void* sanic_hip_buffer_device_ptr(const sanic_hip_buffer* buf) { return buf ? buf->ptr() : nullptr; }
+
+int sanic_hip_wrap(sanic_hip_device* dev, void* device_ptr, size_t bytes, sanic_hip_buffer** out) {
+    return guarded([&] {
+        if (!dev || !out || !device_ptr) fail(SANIC_ERR_ARG, "null argument");
+        auto st = std::make_shared<Storage>();
+        st->ptr = device_ptr;
+        st->bytes = bytes;
+        st->owned = false;
+        auto* b = new sanic_hip_buffer;
+        b->dev = dev;
+        b->storage = st;
+        b->bytes = bytes;
+        *out = b;
+    });
+}
+
+int sanic_hip_prepare(sanic_hip_device* dev, const sanic_program_desc* desc, sanic_hip_exe** out) {
+    return guarded([&] {
+        if (!dev || !desc || !out) fail(SANIC_ERR_ARG, "null argument");
+        *out = nullptr;
+        SANIC_HIP(hipSetDevice(dev->ordinal));
+        auto exe = std::make_unique<sanic_hip_exe>();
+        exe->dev = dev;
+        exe->low = lower_program(desc);
+        exe->buffers.assign(desc->buffers, desc->buffers + desc->n_buffers);
+        for (int s = 0; s < desc->n_stages; s++) {
+            exe->stage_out.push_back(desc->stages[s].out_buffer);
+            exe->stage_out_role.push_back(desc->buffers[desc->stages[s].out_buffer].role);
+        }
+        compile_all(exe.get(), true);
+        *out = exe.release();
+    });
+}
+
+void sanic_hip_exe_free(sanic_hip_exe* exe) { delete exe; }
+
+static int copy_text(const std::string& s, char* out, size_t cap) {
+    if (!out || cap == 0) fail(SANIC_ERR_ARG, "null output");
+    size_t n = std::min(cap - 1, s.size());
+    memcpy(out, s.data(), n);
+    out[n] = 0;
+    if (s.size() >= cap) fail(SANIC_ERR_ARG, "output buffer too small: need " + std::to_string(s.size() + 1));
+    return 0;
+}
+
+int sanic_hip_exe_stage_kernel(const sanic_hip_exe* exe, int stage, char* out, size_t cap) {
+    return guarded([&] {
+        if (!exe || stage < 0 || stage >= (int)exe->low.stages.size()) fail(SANIC_ERR_ARG, "stage out of range");
+        copy_text(exe->low.stages[stage].kernel_kind, out, cap);
+    });
+}
+
+int sanic_hip_exe_stage_source(const sanic_hip_exe* exe, int stage, char* out, size_t cap) {
+    return guarded([&] {
+        if (!exe || stage < 0 || stage >= (int)exe->low.stages.size()) fail(SANIC_ERR_ARG, "stage out of range");
+        copy_text(exe->low.stages[stage].source, out, cap);
+    });
+}
+
+// Allocate the executable-owned buffers (OUTPUT, SCRATCH roles) and the scratch arena.
+static void bind_all(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int n, std::vector<sanic_hip_buffer*>& bound,
+                     std::vector<std::unique_ptr<sanic_hip_buffer>>& owned, std::unique_ptr<sanic_hip_buffer>& scratch) {
+    int nb = (int)exe->buffers.size();
+    if (n != nb) fail(SANIC_ERR_ARG, "expected " + std::to_string(nb) + " bindings, got " + std::to_string(n));
+    bound.assign(nb, nullptr);
+    for (int i = 0; i < nb; i++) {
+        int role = exe->buffers[i].role;
+        if (role == SANIC_BUF_INPUT || role == SANIC_BUF_STATE) {
+            check_binding(exe, i, bindings ? bindings[i] : nullptr);
+            bound[i] = bindings[i];
+        } else {
+            owned.emplace_back(new_buffer(exe->dev, (size_t)buffer_bytes(exe->buffers[i])));
+            bound[i] = owned.back().get();
+        }
+    }
+    scratch.reset(new_buffer(exe->dev, (size_t)std::max<int64_t>(exe->low.scratch_bytes, 256)));
+}
+
+int sanic_hip_execute(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int n_bindings, sanic_hip_buffer** outputs) {
+    return guarded([&] {
+        if (!exe || !outputs) fail(SANIC_ERR_ARG, "null argument");
+        for (int r : exe->stage_out_role)
+            if (r == SANIC_BUF_STATE)
+                fail(SANIC_ERR_IN_PLACE, "this program writes state in place; use capture (compile.rs:745-751)");
+        SANIC_HIP(hipSetDevice(exe->dev->ordinal));
+        std::vector<sanic_hip_buffer*> bound;
+        std::vector<std::unique_ptr<sanic_hip_buffer>> owned;
+        std::unique_ptr<sanic_hip_buffer> scratch;
+        bind_all(exe, bindings, n_bindings, bound, owned, scratch);
+        enqueue(exe, bound, scratch->ptr());
+        SANIC_HIP(hipStreamSynchronize(exe->dev->stream));
+        for (int i = 0; i < (int)exe->buffers.size(); i++) outputs[i] = nullptr;
+        for (auto& o : owned) {
+            for (int i = 0; i < (int)exe->buffers.size(); i++)
+                if (bound[i] == o.get() && exe->buffers[i].role == SANIC_BUF_OUTPUT) outputs[i] = o.release();
+        }
+    });
+}
+
+int sanic_hip_capture(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int n_bindings, const int32_t* feedback,
+                      int n_pairs, sanic_hip_replay** out) {
+    return guarded([&] {
+        if (!exe || !out) fail(SANIC_ERR_ARG, "null argument");
+        *out = nullptr;
+        SANIC_HIP(hipSetDevice(exe->dev->ordinal));
+        auto rp = std::make_unique<sanic_hip_replay>();
+        rp->exe = exe;
+        bind_all(exe, bindings, n_bindings, rp->bound, rp->owned, rp->scratch);
+        int nb = (int)exe->buffers.size();
+        for (int p = 0; p < n_pairs; p++) {
+            int o = feedback[2 * p], i = feedback[2 * p + 1];
+            if (o < 0 || o >= nb || i < 0 || i >= nb) fail(SANIC_ERR_FEEDBACK, "feedback index out of range");
+            const auto& ob = exe->buffers[o];
+            const auto& ib = exe->buffers[i];
+            if (ob.role != SANIC_BUF_OUTPUT && ob.role != SANIC_BUF_SCRATCH)
+                fail(SANIC_ERR_FEEDBACK, "feedback source must be a program output");
+            if (ib.role != SANIC_BUF_INPUT && ib.role != SANIC_BUF_STATE)
+                fail(SANIC_ERR_FEEDBACK, "feedback target must be a bound input");
+            int64_t no = 1, ni = 1;
+            for (int k = 0; k < ob.rank; k++) no *= ob.shape[k];
+            for (int k = 0; k < ib.rank; k++) ni *= ib.shape[k];
+            if (no != ni) fail(SANIC_ERR_FEEDBACK, "feedback pair volumes differ (RunError::Feedback)");
+            rp->feedback.push_back({o, i});
+        }
+        hipStream_t s = exe->dev->stream;
+        SANIC_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        try {
+            enqueue(exe, rp->bound, rp->scratch->ptr());
+            for (auto& fb : rp->feedback) {
+                const auto& ob = exe->buffers[fb.first];
+                const auto& ib = exe->buffers[fb.second];
+                int64_t n = 1;
+                for (int k = 0; k < ob.rank; k++) n *= ob.shape[k];
+                hipLaunchKernelGGL(sanic_convert, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                                   (const void*)rp->bound[fb.first]->ptr(), ob.dtype, (void*)rp->bound[fb.second]->ptr(),
+                                   ib.dtype, n);
+            }
+        } catch (...) {
+            hipGraph_t g;
+            hipStreamEndCapture(s, &g);
+            if (g) hipGraphDestroy(g);
+            throw;
+        }
+        SANIC_HIP(hipStreamEndCapture(s, &rp->graph));
+        SANIC_HIP(hipGraphInstantiate(&rp->graph_exec, rp->graph, nullptr, nullptr, 0));
+        SANIC_HIP(hipEventCreate(&rp->ev0));
+        SANIC_HIP(hipEventCreate(&rp->ev1));
+        *out = rp.release();
+    });
+}
+
+int sanic_hip_replay_buffer(sanic_hip_replay* rp, int index, sanic_hip_buffer** out) {
+    return guarded([&] {
+        if (!rp || !out || index < 0 || index >= (int)rp->bound.size()) fail(SANIC_ERR_ARG, "bad replay buffer index");
+        *out = nullptr;
+        int role = rp->exe->buffers[index].role;
+        if (role != SANIC_BUF_OUTPUT && role != SANIC_BUF_SCRATCH) fail(SANIC_ERR_ARG, "only owned buffers are returned");
+        auto* b = new sanic_hip_buffer(*rp->bound[index]);   // shares the storage
+        *out = b;
+    });
+}
+
+int sanic_hip_step_many(sanic_hip_replay* rp, int n, double* gpu_seconds) {
+    return guarded([&] {
+        if (!rp || n < 1) fail(SANIC_ERR_ARG, "bad replay");
+        hipStream_t s = rp->exe->dev->stream;
+        SANIC_HIP(hipSetDevice(rp->exe->dev->ordinal));
+        SANIC_HIP(hipEventRecord(rp->ev0, s));
+        for (int i = 0; i < n; i++) SANIC_HIP(hipGraphLaunch(rp->graph_exec, s));
+        SANIC_HIP(hipEventRecord(rp->ev1, s));
+        SANIC_HIP(hipEventSynchronize(rp->ev1));
+        float ms = 0;
+        SANIC_HIP(hipEventElapsedTime(&ms, rp->ev0, rp->ev1));
+        if (gpu_seconds) *gpu_seconds = ms * 1e-3;
+    });
+}
+
+int sanic_hip_step(sanic_hip_replay* rp, double* gpu_seconds) { return sanic_hip_step_many(rp, 1, gpu_seconds); }
+
+void sanic_hip_replay_free(sanic_hip_replay* rp) { delete rp; }
+
+int sanic_hip_profile_stages(sanic_hip_replay* rp, double* seconds, int n) {
+    return guarded([&] {
+        if (!rp || !seconds) fail(SANIC_ERR_ARG, "null argument");
+        int ns = (int)rp->exe->low.stages.size();
+        if (n < ns) fail(SANIC_ERR_ARG, "seconds[] is shorter than the stage count");
+        std::vector<hipEvent_t> ev(ns + 1);
+        for (auto& e : ev) SANIC_HIP(hipEventCreate(&e));
+        enqueue(rp->exe, rp->bound, rp->scratch->ptr(), ev.data());
+        SANIC_HIP(hipEventSynchronize(ev[ns]));
+        for (int i = 0; i < ns; i++) {
+            float ms = 0;
+            hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+            seconds[i] = ms * 1e-3;
+        }
+        for (auto& e : ev) hipEventDestroy(e);
+    });
+}
+
+int sanic_hip_sync(sanic_hip_device* dev) {
+    return guarded([&] {
+        if (!dev) fail(SANIC_ERR_ARG, "null device");
+        SANIC_HIP(hipStreamSynchronize(dev->stream));
+    });
+}
+
+// ── device-free entry points: emit and precompile without a GPU ────────────────────────────
+
+int sanic_hip_emit_source(const sanic_program_desc* desc, int stage, char* kind, size_t kcap, char* src, size_t scap) {
+    return guarded([&] {
+        Lowered low = lower_program(desc);
+        if (stage < 0 || stage >= (int)low.stages.size()) fail(SANIC_ERR_ARG, "stage out of range");
+        if (kind) copy_text(low.stages[stage].kernel_kind, kind, kcap);
+        if (src) copy_text(low.stages[stage].source, src, scap);
+    });
+}
+
+int sanic_hip_precompile(const sanic_program_desc* desc) {
+    return guarded([&] {
+        sanic_hip_exe exe;
+        exe.low = lower_program(desc);
+        compile_all(&exe, false);
+    });
+}
+
+size_t sanic_hip_abi_sizeof(const char* name) {
+    std::string n = name ? name : "";
+    if (n == "sanic_node") return sizeof(sanic_node);
+    if (n == "sanic_expr") return sizeof(sanic_expr);
+    if (n == "sanic_slot") return sizeof(sanic_slot);
+    if (n == "sanic_carrier") return sizeof(sanic_carrier);
+    if (n == "sanic_sched") return sizeof(sanic_sched);
+    if (n == "sanic_stage") return sizeof(sanic_stage);
+    if (n == "sanic_buffer_desc") return sizeof(sanic_buffer_desc);
+    if (n == "sanic_program_desc") return sizeof(sanic_program_desc);
+    if (n == "sanic_device_specs") return sizeof(sanic_device_specs);
+    return 0;
+}
+
+}  // extern "C"
