@@ -398,8 +398,21 @@ int oracle_run_stage(const sanic_program_desc* d, int stage, double* const* buff
         ctx_init(&cx, d, buffers, NULL);
         const double* v = eval_node(&cx, st->value);
         const double* w = st->where >= 0 ? eval_node(&cx, st->where) : NULL;
-        for (int64_t i = 0; i < gvol; i++)
-            if (!w || w[i] != 0.0) out[i] = oracle_round_to(st->out_dtype, v[i]);
+        const sanic_node* vn = &d->nodes[st->value];
+        const sanic_node* wn = st->where >= 0 ? &d->nodes[st->where] : NULL;
+        int64_t g[SANIC_MAX_RANK], s[SANIC_MAX_RANK];
+        for (int64_t i = 0; i < gvol; i++) {
+            /* value and condition broadcast against the grid as Map inputs do */
+            unflatten(i, st->grid, st->rank, g);
+            if (w) {
+                int lead = st->rank - wn->rank;
+                for (int j = 0; j < wn->rank; j++) s[j] = wn->shape[j] == 1 ? 0 : g[lead + j];
+                if (w[flatten_at(s, wn->shape, wn->rank)] == 0.0) continue;
+            }
+            int lead = st->rank - vn->rank;
+            for (int j = 0; j < vn->rank; j++) s[j] = vn->shape[j] == 1 ? 0 : g[lead + j];
+            out[i] = oracle_round_to(st->out_dtype, v[flatten_at(s, vn->shape, vn->rank)]);
+        }
         ctx_free(&cx);
     }
     free(val);

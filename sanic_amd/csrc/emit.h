@@ -25,6 +25,7 @@ struct Renderer {
     std::vector<std::map<std::string, std::string>> memo;  // scoped common-subexpression cache
     int tmp = 0;
     std::string fold_var = "fold_v";
+    std::map<int, std::string> subst;            // node id -> precomputed value expression
     explicit Renderer(const sanic_program_desc* dd) : d(dd) { memo.emplace_back(); }
 
     std::string param(int buffer);

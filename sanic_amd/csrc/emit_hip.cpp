@@ -15,6 +15,7 @@
 // All arithmetic is f32 (accumulators included); loads widen from the storage dtype and the
 // single store narrows through it (emit_metal.rs:162-232).
 #include "emit.h"
+#include "skeletons.h"
 
 #include <algorithm>
 #include <cmath>
@@ -383,6 +384,8 @@ std::string Renderer::load(int node, const std::vector<std::string>& c) {
 // expression (usually a fresh local) holding the f32 value.
 std::string Renderer::value(Code& code, int node, const std::vector<std::string>& c) {
     const sanic_node& n = d->nodes[node];
+    auto sb = subst.find(node);
+    if (sb != subst.end()) return sb->second;
     std::string key = std::to_string(node) + "@";
     for (auto& x : c) key += x + ",";
     for (auto it = memo.rbegin(); it != memo.rend(); ++it) {
@@ -435,7 +438,7 @@ std::string Renderer::value(Code& code, int node, const std::vector<std::string>
         const sanic_node& x = d->nodes[n.in[1]];
         std::vector<std::string> ic(c.begin() + n.dim, c.begin() + n.dim + x.rank);
         std::string iv = value(code, n.in[1], ic);
-        std::string gi = fresh("g");
+        std::string gi = fresh("gx");
         // round half away from zero (f64::round), clamped so a bad index cannot fault
         code.line("idx_t " + gi + " = (idx_t)roundf(" + iv + ");");
         code.line(gi + " = " + gi + " < 0 ? 0 : (" + gi + " > " + std::to_string(s.shape[n.dim] - 1) + " ? " +
@@ -482,7 +485,7 @@ std::string Renderer::value(Code& code, int node, const std::vector<std::string>
                 int64_t span = coef * (n.shape[od] - 1);
                 if (span < 0) lo += span; else hi += span;
             }
-            std::string v = fresh("x");
+            std::string v = fresh("ix");
             code.line("const idx_t " + v + " = " + e + ";");
             sc[j] = v;
             if (n.padded && (lo < 0 || hi >= s.shape[j])) {
@@ -935,18 +938,26 @@ LoweredStage lower_pointwise(const sanic_program_desc* d, int si) {
 Lowered lower_program(const sanic_program_desc* d) {
     validate(d);
     Lowered out;
-    for (int s = 0; s < d->n_stages; s++) {
+    for (int s = 0; s < d->n_stages;) {
         const sanic_stage& st = d->stages[s];
-        LoweredStage L;
-        bool done = false;
         if (st.kind == SANIC_STAGE_FUSED) {
-            done = lower_skeleton(d, s, out.scratch_bytes, L);
-            if (!done) L = lower_generic_fold(d, s, out.scratch_bytes);
+            std::vector<LoweredStage> grp;
+            if (!getenv("SANIC_HIP_GENERIC") && lower_gemv_group(d, s, out.scratch_bytes, grp)) {
+                for (auto& g : grp) out.stages.push_back(std::move(g));
+                s += (int)grp.size();
+                continue;
+            }
+            LoweredStage L;
+            if (getenv("SANIC_HIP_GENERIC") || !lower_skeleton(d, s, out.scratch_bytes, L))
+                L = lower_generic_fold(d, s, out.scratch_bytes);
+            out.stages.push_back(std::move(L));
         } else {
-            done = lower_pointwise_skeleton(d, s, out.scratch_bytes, L);
-            if (!done) L = lower_pointwise(d, s);
+            LoweredStage L;
+            if (getenv("SANIC_HIP_GENERIC") || !lower_pointwise_skeleton(d, s, out.scratch_bytes, L))
+                L = lower_pointwise(d, s);
+            out.stages.push_back(std::move(L));
         }
-        out.stages.push_back(std::move(L));
+        s++;
     }
     return out;
 }

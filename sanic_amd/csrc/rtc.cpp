@@ -58,10 +58,15 @@ std::string compile_source(const std::string& source) {
     std::string code;
     if (!getenv("SANIC_HIP_NO_CACHE") && read_file(path, code)) return code;
 
+    static std::mutex create_mu;
     hiprtcProgram prog;
-    if (hiprtcCreateProgram(&prog, source.c_str(), "sanic_kernel.hip", 0, nullptr, nullptr) !=
-        HIPRTC_SUCCESS)
-        fail(SANIC_ERR_COMPILE, "hiprtcCreateProgram failed");
+    hiprtcResult cr;
+    {
+        std::lock_guard<std::mutex> lk(create_mu);
+        cr = hiprtcCreateProgram(&prog, source.c_str(), "sanic_kernel.hip", 0, nullptr, nullptr);
+    }
+    if (cr != HIPRTC_SUCCESS)
+        fail(SANIC_ERR_COMPILE, std::string("hiprtcCreateProgram failed: ") + hiprtcGetErrorString(cr));
     hiprtcResult r = hiprtcCompileProgram(prog, (int)(sizeof kOptions / sizeof *kOptions), kOptions);
     if (r != HIPRTC_SUCCESS) {
         size_t n = 0;

@@ -163,7 +163,7 @@ static sanic_hip_buffer* new_buffer(sanic_hip_device* dev, size_t bytes) {
 static void compile_all(sanic_hip_exe* exe, bool load) {
     std::vector<std::string> sources;
     for (auto& s : exe->low.stages)
-        if (!exe->modules.count(s.source)) {
+        if (!s.launches.empty() && !exe->modules.count(s.source)) {
             exe->modules[s.source] = std::make_shared<Module>();
             sources.push_back(s.source);
         }

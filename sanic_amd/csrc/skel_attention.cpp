@@ -1,0 +1,500 @@
+// Attention skeletons: the online-softmax (m, ℓ, o) carrier over a streamed key axis.
+//
+// Accepted structurally (derive.rs:518-530 slot kinds, the FlashAttention carrier of
+// /root/reference/tests/laws.rs:108-126): one Plain(Max) slot whose `into` is a score item, the
+// other slots ExpShifted on it with `into` either a constant (ℓ) or the value item (o); the
+// score leaf contains exactly one in-body contraction Σ_d A·B where A (the query side) does not
+// move with the stream and B (the key side) is an affine view of one buffer; the value leaf is
+// an affine view too. GQA is read off the key/value addresses: when the head coordinate enters
+// them as ⌊h / rep⌋, the `rep` query heads that share a key row are processed together so each
+// K/V byte is read once.
+//
+//   attn_decode  (query grid = heads only) Flash-Decoding: the visible stream (honest window)
+//                is cut into 64-position chunks, one workgroup per (KV head group, chunk) folds
+//                its chunk into partial (m, ℓ, o) carriers in scratch; a second kernel merges the
+//                partials with the carrier's own rendered combine (−∞ guard included), projects,
+//                runs the epilogue and stores. Oracle: interp.rs:555-643 run_carrier_split.
+#include <algorithm>
+#include <cmath>
+
+#include "emit.h"
+#include "skeletons.h"
+
+namespace sanic {
+
+namespace {
+
+struct Dot {
+    int reduce = -1;     // the Reduce(Add) node
+    int a = -1, b = -1;  // query side (A) / key side (B) children of its Map(Mul)
+    std::vector<std::string> a_coords;  // A coords in terms of "hq", "dd" (and 0)
+    Access kacc;         // B address over vars {0: h, 1: t, 2: d}
+    int64_t depth = 0;   // contraction length
+};
+
+struct AttnPlan {
+    int stage = -1;
+    int sleaf = -1, vleaf = -1;
+    int max_slot = -1;
+    std::vector<int> vec_slots, scalar_slots;
+    std::vector<double> scalar_into;
+    int hdim = -1, edim = -1;
+    int64_t NH = 1, E = 1, T = 1;
+    int rep = 1;
+    Dot dot;
+    Access vacc;         // V address over vars {0: h, 1: t, 2: e}
+};
+
+bool expr_is_item(const sanic_program_desc* d, int e, int& item) {
+    const sanic_expr& x = d->exprs[e];
+    if (x.op != SANIC_EX_ITEM) return false;
+    item = x.index;
+    return true;
+}
+
+bool expr_is_const(const sanic_program_desc* d, int e, double& v) {
+    const sanic_expr& x = d->exprs[e];
+    if (x.op != SANIC_EX_CONST) return false;
+    v = x.value;
+    return true;
+}
+
+bool contains_reduce(const sanic_program_desc* d, int node) {
+    const sanic_node& n = d->nodes[node];
+    if (n.kind == SANIC_NODE_REDUCE) return true;
+    for (int k = 0; k < n.n_in; k++) if (contains_reduce(d, n.in[k])) return true;
+    return false;
+}
+
+bool sym_uses(const Sym& s, int var) {
+    for (auto& t : s.terms) if (t.var == var) return true;
+    return false;
+}
+
+// Find the single contraction in the score tree. `c` are the node's coords over {h, t}.
+bool find_dot(const sanic_program_desc* d, int node, const std::vector<Sym>& c, const std::vector<int64_t>& ext, Dot& out) {
+    const sanic_node& n = d->nodes[node];
+    if (n.kind == SANIC_NODE_MAP) {
+        int found = 0;
+        for (int k = 0; k < n.n_in; k++) {
+            if (!contains_reduce(d, n.in[k])) continue;
+            const sanic_node& m = d->nodes[n.in[k]];
+            int lead = n.rank - m.rank;
+            std::vector<Sym> cc(m.rank);
+            for (int j = 0; j < m.rank; j++) cc[j] = m.shape[j] == 1 ? Sym() : c[lead + j];
+            if (!find_dot(d, n.in[k], cc, ext, out)) return false;
+            found++;
+        }
+        return found == 1;
+    }
+    if (n.kind != SANIC_NODE_REDUCE || n.op != SANIC_MON_ADD) return false;
+    const sanic_node& mp = d->nodes[n.in[0]];
+    if (mp.kind != SANIC_NODE_MAP || mp.op != SANIC_OP_MUL) return false;
+    std::vector<Sym> mc;
+    for (int j = 0, o = 0; j < mp.rank; j++) mc.push_back(j == n.dim ? Sym::var(2) : c[o++]);
+    std::vector<int64_t> ext3 = {ext[0], ext[1], mp.shape[n.dim]};
+    int kside = -1;
+    std::vector<std::vector<Sym>> childc(2);
+    for (int k = 0; k < 2; k++) {
+        const sanic_node& ch = d->nodes[mp.in[k]];
+        int lead = mp.rank - ch.rank;
+        childc[k].resize(ch.rank);
+        bool moves = false;
+        for (int j = 0; j < ch.rank; j++) {
+            childc[k][j] = ch.shape[j] == 1 ? Sym() : mc[lead + j];
+            moves |= sym_uses(childc[k][j], 1);
+        }
+        if (moves) {
+            if (kside >= 0) return false;
+            kside = k;
+        }
+    }
+    if (kside < 0) return false;
+    int qside = 1 - kside;
+    if (!sym_access(d, mp.in[kside], childc[kside], ext3, out.kacc)) return false;
+    // query-side coords as strings: h -> "hq", d -> "dd"
+    const auto& qc = childc[qside];
+    for (auto& s : qc) {
+        if (s.terms.empty()) { out.a_coords.push_back(std::to_string(s.c0)); continue; }
+        if (s.terms.size() != 1 || s.c0 != 0 || s.terms[0].coef != 1 || s.terms[0].div != 1 || s.terms[0].mod) return false;
+        out.a_coords.push_back(s.terms[0].var == 0 ? "hq" : s.terms[0].var == 2 ? "dd" : "??");
+        if (s.terms[0].var == 1) return false;
+    }
+    out.reduce = node;
+    out.a = mp.in[qside];
+    out.b = mp.in[kside];
+    out.depth = mp.shape[n.dim];
+    return true;
+}
+
+// Split an address into (h term div, stride of var v) — h may enter only as ⌊h/rep⌋.
+bool addr_parts(const Sym& a, int& rep, int64_t NH, int64_t& s1, int64_t& s2, int64_t& sh) {
+    rep = (int)NH;   // no h term: every head reads the same rows
+    s1 = s2 = sh = 0;
+    for (auto& t : a.terms) {
+        if (t.mod != 0) return false;
+        if (t.var == 0) {
+            if (t.div < 1 || NH % t.div) return false;
+            rep = (int)t.div;
+            sh = t.coef;
+        } else if (t.div != 1) {
+            return false;
+        } else if (t.var == 1) {
+            s1 += t.coef;
+        } else {
+            s2 += t.coef;
+        }
+    }
+    return true;
+}
+
+bool attn_plan(const sanic_program_desc* d, int si, AttnPlan& P) {
+    const sanic_stage& st = d->stages[si];
+    if (st.kind != SANIC_STAGE_FUSED) return false;
+    const sanic_carrier& c = st.carrier;
+    P = AttnPlan();
+    P.stage = si;
+    for (int k = 0; k < c.slots; k++) {
+        const sanic_slot& s = c.kind[k];
+        if (s.kind == SANIC_SLOT_PLAIN && s.monoid == SANIC_MON_MAX) {
+            if (P.max_slot >= 0) return false;
+            P.max_slot = k;
+        }
+    }
+    if (P.max_slot < 0) return false;
+    if (!expr_is_item(d, c.into[P.max_slot], P.sleaf)) return false;
+    for (int k = 0; k < c.slots; k++) {
+        if (k == P.max_slot) continue;
+        const sanic_slot& s = c.kind[k];
+        if (s.kind != SANIC_SLOT_EXP_SHIFTED || s.ref_slot != P.max_slot) return false;
+        int it;
+        double v;
+        if (expr_is_item(d, c.into[k], it)) {
+            if (it == P.sleaf) return false;
+            if (P.vleaf >= 0 && P.vleaf != it) return false;
+            P.vleaf = it;
+            P.vec_slots.push_back(k);
+        } else if (expr_is_const(d, c.into[k], v)) {
+            P.scalar_slots.push_back(k);
+            P.scalar_into.push_back(v);
+        } else {
+            return false;
+        }
+    }
+    if (P.vleaf < 0 || P.vec_slots.empty() || st.n_leaves != 2) return false;
+    // grid: value dim = bound by the value leaf only; head dim = the other dim with extent > 1
+    const sanic_node& sl = d->nodes[st.leaf[P.sleaf]];
+    const sanic_node& vl = d->nodes[st.leaf[P.vleaf]];
+    std::vector<bool> in_s(st.rank, false), in_v(st.rank, false);
+    for (int j = 0; j < sl.rank; j++) if (st.bind[P.sleaf][j] >= 0) in_s[st.bind[P.sleaf][j]] = true;
+    for (int j = 0; j < vl.rank; j++) if (st.bind[P.vleaf][j] >= 0) in_v[st.bind[P.vleaf][j]] = true;
+    for (int j = 0; j < st.rank; j++) {
+        if (st.grid[j] == 1) continue;
+        if (in_v[j] && !in_s[j]) {
+            if (P.edim >= 0) return false;
+            P.edim = j;
+        } else {
+            if (P.hdim >= 0) return false;
+            P.hdim = j;
+        }
+    }
+    if (P.edim < 0) return false;
+    P.E = st.grid[P.edim];
+    P.NH = P.hdim >= 0 ? st.grid[P.hdim] : 1;
+    P.T = st.stream;
+    if (P.E > 256) return false;
+    // the score leaf's contraction
+    std::vector<Sym> sc(sl.rank);
+    for (int j = 0; j < sl.rank; j++) {
+        int b = st.bind[P.sleaf][j];
+        sc[j] = b == SANIC_BIND_STREAM ? Sym::var(1) : (b >= 0 && b == P.hdim) ? Sym::var(0) : Sym();
+    }
+    if (!find_dot(d, st.leaf[P.sleaf], sc, {P.NH, P.T}, P.dot)) return false;
+    // value address over {h, t, e}
+    std::vector<Sym> vc(vl.rank);
+    for (int j = 0; j < vl.rank; j++) {
+        int b = st.bind[P.vleaf][j];
+        vc[j] = b == SANIC_BIND_STREAM ? Sym::var(1) : b == P.hdim ? Sym::var(0) : b == P.edim ? Sym::var(2) : Sym();
+    }
+    if (!sym_access(d, st.leaf[P.vleaf], vc, {P.NH, P.T, P.E}, P.vacc)) return false;
+    int repk, repv;
+    int64_t kt, kd, kh, vt, ve, vh;
+    if (!addr_parts(P.dot.kacc.addr, repk, P.NH, kt, kd, kh)) return false;
+    if (!addr_parts(P.vacc.addr, repv, P.NH, vt, ve, vh)) return false;
+    if (repk != repv || kd != 1 || P.dot.kacc.dtype != SANIC_BF16 || P.vacc.dtype != SANIC_BF16) return false;
+    if (P.dot.depth % 8 || P.dot.depth > 256) return false;
+    P.rep = repk;
+    if (P.rep > 8) return false;
+    return true;
+}
+
+}  // namespace
+
+bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
+    AttnPlan P;
+    if (!attn_plan(d, si, P)) return false;
+    const sanic_stage& st = d->stages[si];
+    const sanic_carrier& c = st.carrier;
+    const int REP = P.rep;
+    const int64_t HD = P.dot.depth, E = P.E, T = P.T, NH = P.NH;
+    const int64_t NG = NH / REP;
+    const int CH = 64;                            // stream positions per workgroup
+    const int64_t NCH = (T + CH - 1) / CH;
+    const int NS = (int)P.scalar_slots.size(), NV = (int)P.vec_slots.size();
+    const int PSZ = 1 + NS + NV * (int)E;         // floats per (chunk, head) partial
+    int64_t part_off = scratch;
+    scratch += ((NCH * NH * PSZ * 4 + 255) / 256) * 256;
+
+    Renderer R(d);
+    Code k;
+    k.indent = 1;
+    k.line("__shared__ float q_lds[" + std::to_string(REP * HD) + "];");
+    k.line("__shared__ float p_lds[" + std::to_string(REP) + "][" + std::to_string(CH) + "];");
+    k.line("__shared__ float stat_lds[" + std::to_string(REP) + "][2];");
+    k.line("__shared__ float o_lds[4][" + std::to_string(REP) + "][" + std::to_string(E) + "];");
+    k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
+    k.line("const idx_t grp = blockIdx.x, chunk = blockIdx.y;");
+    // honest window (per first head of the group; bounds not depending on the head)
+    auto win = honest_window(d, st);
+    k.line("idx_t lo0 = 0, hi0 = " + std::to_string(T) + ";");
+    {
+        Code wc;
+        wc.indent = 1;
+        R.memo.emplace_back();
+        // evaluate window edges with grid coords g* = first head of the group, e = 0
+        for (int j = 0; j < st.rank; j++)
+            wc.line("const idx_t g" + std::to_string(j) + " = " + (j == P.hdim ? "grp * " + std::to_string(REP) : std::string("0")) + ";");
+        emit_window(R, wc, st, win, "wlo", "whi");
+        wc.line("lo0 = wlo; hi0 = whi;");
+        R.memo.pop_back();
+        k.line("{");
+        k.s << wc.str();
+        k.line("}");
+    }
+    k.line("const idx_t t0 = lo0 + chunk * " + std::to_string(CH) + ";");
+    k.line("float* part = a.scratch + (chunk * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + ") * " + std::to_string(PSZ) + ";");
+    // identity partial for chunks past the visible window
+    k.line("if (t0 >= hi0) {");
+    k.line("  for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += 256) {");
+    k.line("    const int r = i / " + std::to_string(PSZ) + ", f = i % " + std::to_string(PSZ) + ";");
+    k.line("    part[r * " + std::to_string(PSZ) + " + f] = f == 0 ? " + flit(c.identity[P.max_slot]) + " : 0.0f;");
+    k.line("  }");
+    k.line("  return;");
+    k.line("}");
+    k.line("const idx_t t1 = t0 + " + std::to_string(CH) + " < hi0 ? t0 + " + std::to_string(CH) + " : hi0;");
+    // query vectors (the A side, rendered) into LDS
+    k.line("for (int i = tid; i < " + std::to_string(REP * HD) + "; i += 256) {");
+    k.indent++;
+    k.line("const idx_t hq = grp * " + std::to_string(REP) + " + i / " + std::to_string(HD) + ";");
+    k.line("const idx_t dd = i % " + std::to_string(HD) + ";");
+    {
+        R.memo.emplace_back();
+        std::string v = R.value(k, P.dot.a, P.dot.a_coords);
+        R.memo.pop_back();
+        k.line("q_lds[i] = " + v + ";");
+    }
+    k.indent--;
+    k.line("}");
+    k.line("__syncthreads();");
+    // scores: LPT lanes per position, each lane DPL = HD / LPT contiguous d
+    const int LPT = 4;
+    const int64_t DPL = HD / LPT;
+    const int64_t TPP = 256 / LPT;   // positions per pass
+    int repk; int64_t kt, kd, kh;
+    addr_parts(P.dot.kacc.addr, repk, NH, kt, kd, kh);
+    int64_t kbase = P.dot.kacc.addr.c0;
+    k.line("const unsigned short* __restrict__ kp = " + R.param(P.dot.kacc.buffer) + " + " + std::to_string(kbase) + " + grp * " + std::to_string(kh) + ";");
+    k.line("for (int pass = 0; pass < " + std::to_string((CH + TPP - 1) / TPP) + "; ++pass) {");
+    k.indent++;
+    k.line("const int tl = pass * " + std::to_string(TPP) + " + tid / " + std::to_string(LPT) + ";");
+    k.line("const int sub = tid % " + std::to_string(LPT) + ";");
+    k.line("const idx_t t = t0 + tl;");
+    k.line("float dot[" + std::to_string(REP) + "];");
+    k.line("#pragma unroll");
+    k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) dot[r] = 0.0f;");
+    k.line("if (tl < " + std::to_string(CH) + " && t < t1) {");
+    k.indent++;
+    k.line("#pragma unroll");
+    k.line("for (int v8 = 0; v8 < " + std::to_string(DPL / 8) + "; ++v8) {");
+    k.indent++;
+    k.line("const int d0 = sub * " + std::to_string(DPL) + " + v8 * 8;");
+    k.line("const uint4 kv = *(const uint4*)(kp + t * " + std::to_string(kt) + " + d0);");
+    k.line("const float kf[8] = {__uint_as_float(kv.x << 16), __uint_as_float(kv.x & 0xFFFF0000u), __uint_as_float(kv.y << 16), __uint_as_float(kv.y & 0xFFFF0000u), __uint_as_float(kv.z << 16), __uint_as_float(kv.z & 0xFFFF0000u), __uint_as_float(kv.w << 16), __uint_as_float(kv.w & 0xFFFF0000u)};");
+    k.line("#pragma unroll");
+    k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r)");
+    k.line("  #pragma unroll");
+    k.line("  for (int j = 0; j < 8; ++j) dot[r] = fmaf(q_lds[r * " + std::to_string(HD) + " + d0 + j], kf[j], dot[r]);");
+    k.indent--;
+    k.line("}");
+    k.indent--;
+    k.line("}");
+    k.line("#pragma unroll");
+    k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) {");
+    k.line("  #pragma unroll");
+    k.line("  for (int off = 1; off < " + std::to_string(LPT) + "; off <<= 1) dot[r] += __shfl_xor(dot[r], off, 64);");
+    k.line("}");
+    k.line("if (sub == 0 && tl < " + std::to_string(CH) + ") {");
+    k.indent++;
+    k.line("const idx_t s = t;");
+    for (int r = 0; r < REP; r++) {
+        // the score at (h = grp·REP + r, t): the leaf with its contraction substituted
+        k.line("{");
+        k.indent++;
+        k.line("const float dotv = dot[" + std::to_string(r) + "];");
+        R.memo.emplace_back();
+        R.subst[P.dot.reduce] = "dotv";
+        const sanic_node& sl = d->nodes[st.leaf[P.sleaf]];
+        std::vector<std::string> lc(sl.rank);
+        for (int j = 0; j < sl.rank; j++) {
+            int b = st.bind[P.sleaf][j];
+            lc[j] = b == SANIC_BIND_STREAM ? "s" : b == P.hdim ? "(grp * " + std::to_string(REP) + " + " + std::to_string(r) + ")" : "0";
+        }
+        std::string v = R.value(k, st.leaf[P.sleaf], lc);
+        R.subst.clear();
+        R.memo.pop_back();
+        k.line("p_lds[" + std::to_string(r) + "][tl] = t < t1 ? " + v + " : (-__builtin_huge_valf());");
+        k.indent--;
+        k.line("}");
+    }
+    k.indent--;
+    k.line("}");
+    k.indent--;
+    k.line("}");
+    k.line("__syncthreads();");
+    // per head: max, p = exp(s − m) (0 when m = −∞), Σ p
+    k.line("for (int r = wv; r < " + std::to_string(REP) + "; r += 4) {");
+    k.indent++;
+    k.line("float m = (-__builtin_huge_valf());");
+    k.line("for (int i = lane; i < " + std::to_string(CH) + "; i += 64) m = fmaxf(m, p_lds[r][i]);");
+    k.line("for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));");
+    k.line("float l = 0.0f;");
+    k.line("for (int i = lane; i < " + std::to_string(CH) + "; i += 64) {");
+    k.line("  const float p = m == (-__builtin_huge_valf()) ? 0.0f : expf(p_lds[r][i] - m);");
+    k.line("  p_lds[r][i] = p;");
+    k.line("  l += p;");
+    k.line("}");
+    k.line("for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);");
+    k.line("if (lane == 0) { stat_lds[r][0] = m; stat_lds[r][1] = l; }");
+    k.indent--;
+    k.line("}");
+    k.line("__syncthreads();");
+    // o[r][e] = Σ_t p[r][t] · V(h, t, e)
+    int repv; int64_t vt, ve, vh;
+    addr_parts(P.vacc.addr, repv, NH, vt, ve, vh);
+    int64_t vbase = P.vacc.addr.c0;
+    k.line("const unsigned short* __restrict__ vp = " + R.param(P.vacc.buffer) + " + " + std::to_string(vbase) + " + grp * " + std::to_string(vh) + ";");
+    k.line("for (int e = tid % 64; e < " + std::to_string(E) + "; e += 64) {");
+    k.indent++;
+    k.line("const int tg = tid / 64;");   // 4 groups of 16 positions
+    k.line("float o[" + std::to_string(REP) + "];");
+    k.line("#pragma unroll");
+    k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = 0.0f;");
+    k.line("const int tbase = tg * 16;");
+    if (vt == 1) {
+        k.line("if (t0 + tbase + 16 <= t1) {");
+        k.line("  const uint4 va = *(const uint4*)(vp + e * " + std::to_string(ve) + " + t0 + tbase);");
+        k.line("  const uint4 vb = *(const uint4*)(vp + e * " + std::to_string(ve) + " + t0 + tbase + 8);");
+        k.line("  const unsigned vw[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};");
+        k.line("  #pragma unroll");
+        k.line("  for (int j = 0; j < 16; ++j) {");
+        k.line("    const float vf = __uint_as_float((j & 1) ? (vw[j >> 1] & 0xFFFF0000u) : (vw[j >> 1] << 16));");
+        k.line("    #pragma unroll");
+        k.line("    for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = fmaf(p_lds[r][tbase + j], vf, o[r]);");
+        k.line("  }");
+        k.line("} else {");
+        k.line("  for (int j = 0; j < 16; ++j) {");
+        k.line("    const idx_t t = t0 + tbase + j;");
+        k.line("    if (t < t1) {");
+        k.line("      const float vf = sanic_bf16(vp[e * " + std::to_string(ve) + " + t]);");
+        k.line("      for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = fmaf(p_lds[r][tbase + j], vf, o[r]);");
+        k.line("    }");
+        k.line("  }");
+        k.line("}");
+    } else {
+        k.line("for (int j = 0; j < 16; ++j) {");
+        k.line("  const idx_t t = t0 + tbase + j;");
+        k.line("  if (t < t1) {");
+        k.line("    const float vf = sanic_bf16(vp[e * " + std::to_string(ve) + " + t * " + std::to_string(vt) + "]);");
+        k.line("    for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = fmaf(p_lds[r][tbase + j], vf, o[r]);");
+        k.line("  }");
+        k.line("}");
+    }
+    k.line("#pragma unroll");
+    k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) o_lds[tg][r][e] = o[r];");
+    k.indent--;
+    k.line("}");
+    k.line("__syncthreads();");
+    // write the partial carriers: [m, scalar slots (into·ℓ), vector slots (o)]
+    k.line("for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += 256) {");
+    k.indent++;
+    k.line("const int r = i / " + std::to_string(PSZ) + ", f = i % " + std::to_string(PSZ) + ";");
+    k.line("float v;");
+    k.line("if (f == 0) v = stat_lds[r][0];");
+    for (int s = 0; s < NS; s++)
+        k.line("else if (f == " + std::to_string(1 + s) + ") v = " + flit(P.scalar_into[s]) + " * stat_lds[r][1];");
+    k.line("else { const int e = (f - " + std::to_string(1 + NS) + ") % " + std::to_string(E) + "; v = ((o_lds[0][r][e] + o_lds[1][r][e]) + o_lds[2][r][e]) + o_lds[3][r][e]; }");
+    k.line("part[r * " + std::to_string(PSZ) + " + f] = v;");
+    k.indent--;
+    k.line("}");
+
+    // merge kernel: one lane per output point
+    Code m;
+    m.indent = 1;
+    int64_t gvol = 1;
+    for (int j = 0; j < st.rank; j++) gvol *= st.grid[j];
+    m.line("const idx_t gid = (idx_t)blockIdx.x * 256 + threadIdx.x;");
+    m.line("if (gid >= " + std::to_string(gvol) + ") return;");
+    decode_grid(m, st, "gid");
+    std::string hexpr = P.hdim >= 0 ? "g" + std::to_string(P.hdim) : "0";
+    std::string eexpr = "g" + std::to_string(P.edim);
+    // slot -> partial field
+    auto field = [&](int slot) -> std::string {
+        if (slot == P.max_slot) return "0";
+        for (int s = 0; s < NS; s++) if (P.scalar_slots[s] == slot) return std::to_string(1 + s);
+        for (int v = 0; v < NV; v++) if (P.vec_slots[v] == slot) return std::to_string(1 + NS + v * E) + " + " + eexpr;
+        return "0";
+    };
+    m.line("const float* pp = a.scratch + " + hexpr + " * " + std::to_string(PSZ) + ";");
+    for (int s = 0; s < c.slots; s++) m.line("float acc" + std::to_string(s) + " = pp[" + field(s) + "];");
+    m.line("for (idx_t ch = 1; ch < " + std::to_string(NCH) + "; ++ch) {");
+    m.indent++;
+    m.line("const float* q = pp + ch * " + std::to_string(NH * PSZ) + ";");
+    for (int s = 0; s < c.slots; s++) m.line("const float o" + std::to_string(s) + " = q[" + field(s) + "];");
+    m.line("{");
+    m.indent++;
+    for (int s = 0; s < c.slots; s++) {
+        std::string v = R.expr(m, c.combine[s], "", "acc", "o", "");
+        m.line("const float nx" + std::to_string(s) + " = " + v + ";");
+    }
+    for (int s = 0; s < c.slots; s++) m.line("acc" + std::to_string(s) + " = nx" + std::to_string(s) + ";");
+    m.indent--;
+    m.line("}");
+    m.indent--;
+    m.line("}");
+    std::string f = R.expr(m, c.project, "", "", "", "acc");
+    m.line("const float fold_v = " + f + ";");
+    std::string v = "fold_v";
+    if (st.epilogue >= 0) {
+        std::vector<std::string> gc;
+        for (int j = 0; j < st.rank; j++) gc.push_back("g" + std::to_string(j));
+        R.fold_var = "fold_v";
+        R.memo.emplace_back();
+        v = R.value(m, st.epilogue, gc);
+        R.memo.pop_back();
+    }
+    m.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v));
+
+    std::ostringstream src;
+    src << kPrelude << R.args_struct({"float* __restrict__ scratch"});
+    src << "extern \"C\" __global__ void __launch_bounds__(256) sanic_attn_decode(Args a) {\n" << k.str() << "}\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) sanic_attn_merge(Args a) {\n" << m.str() << "}\n";
+    out.kernel_kind = "skeleton:attn_decode[rep " + std::to_string(REP) + "]";
+    out.source = src.str();
+    std::vector<Arg> args = R.arg_list();
+    args.push_back({Arg::SCRATCH, part_off});
+    out.launches.push_back({"sanic_attn_decode", "", dim3((unsigned)NG, (unsigned)NCH), dim3(256), 0, args});
+    out.launches.push_back({"sanic_attn_merge", "", dim3((unsigned)((gvol + 255) / 256)), dim3(256), 0, args});
+    return true;
+}
+
+}  // namespace sanic

@@ -1,0 +1,46 @@
+// Structural analysis shared by the skeletons: symbolic affine coordinates and accesses.
+#pragma once
+#include <string>
+#include <vector>
+
+#include "emit.h"
+
+namespace sanic {
+
+// coef · ((var / div) % mod); mod 0 = none
+struct SymTerm {
+    int64_t coef;
+    int var;
+    int64_t div;
+    int64_t mod;
+};
+
+// c0 + Σ terms: an integer coordinate as a function of kernel variables
+struct Sym {
+    int64_t c0 = 0;
+    std::vector<SymTerm> terms;
+    static Sym var(int v);
+    std::string render(const std::vector<std::string>& vars) const;
+};
+
+// An Input read through Reindex/View chains, as element address = Sym.
+struct Access {
+    int buffer = -1, dtype = -1, node = -1;
+    Sym addr;
+};
+
+// The element address of `node` at symbolic coordinates `c` (ext = extent of each variable);
+// false when the node is not an affine view of one input (or a padded read may go out of
+// bounds).
+bool sym_access(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
+                const std::vector<int64_t>& ext, Access& out);
+
+bool sym_child_coords(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
+                      const std::vector<int64_t>& ext, std::vector<Sym>& sc);
+
+bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out);
+
+// Lower stage `si` (and the following stages it batches with) onto the gemv skeleton.
+bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std::vector<LoweredStage>& out);
+
+}  // namespace sanic

@@ -1,0 +1,75 @@
+"""Stateful decode over the HIP backend: the `Graph::compile_for` → `instantiate` →
+`Machine::step` path (/root/reference/src/graph.rs:231-345) for the Llama-3.2 decode program.
+
+States (the K/V caches and the position) are allocated and zeroed at instantiation
+(graph.rs:297-310); one step is one hipGraph replay; the greedy token is fed back into the
+`tokens` input inside the graph (the reference's feedback binding, compile.rs:869-961), so
+decode steps launch back to back with no host round trip. Prompt tokens are written by the host
+before each prefill step, as the reference's token-by-token prefill does
+(/root/reference/examples/llama3_2.rs:587-680).
+"""
+from __future__ import annotations
+
+import struct
+from typing import Dict, List, Optional
+
+import numpy as np
+
+from . import configs, ir
+from .backend import Buffer, HipDevice
+from .program import STATE
+
+
+class LlamaMachine:
+    def __init__(self, dev: HipDevice, weights: Dict[str, Buffer],
+                 shape: configs.LlamaShape = configs.LLAMA_1B, attn_sched=None):
+        self.dev = dev
+        self.shape = shape
+        self.prog = configs.llama_decode(shape, attn_sched=attn_sched)
+        self.exe = dev.prepare(self.prog)
+        self.bind: Dict[str, Buffer] = dict(weights)
+        self.tokens = dev.alloc(4)
+        self.bind["tokens"] = self.tokens
+        for b in self.prog.buffers:
+            if b.role == STATE:
+                buf = dev.alloc(b.nbytes)
+                buf.upload(bytes(b.nbytes))          # states start at zero
+                self.bind[b.name] = buf
+        self.replay = self.exe.capture(self.bind, feedback=[("token", "tokens")])
+        self.logits = self.replay.buffer("logits")
+        self.token = self.replay.buffer("token")
+
+    def set_position(self, pos: int):
+        self.bind["position"].upload(struct.pack("<f", float(pos)))
+
+    def position(self) -> int:
+        return int(struct.unpack("<f", self.bind["position"].download(4))[0])
+
+    def set_token(self, tok: int):
+        self.tokens.upload(struct.pack("<f", float(tok)))
+
+    def step(self, token: Optional[int] = None) -> float:
+        """One decode step; `token` overrides the fed-back token (prefill). Returns GPU s."""
+        if token is not None:
+            self.set_token(token)
+        return self.replay.step()
+
+    def prefill(self, prompt: List[int]) -> int:
+        """Token-by-token prefill; returns the greedy token after the last prompt token."""
+        for t in prompt:
+            self.step(t)
+        return self.last_token()
+
+    def decode(self, n: int) -> float:
+        """n greedy steps back to back (each step's token feeds the next); GPU seconds."""
+        return self.replay.step_many(n)
+
+    def last_token(self) -> int:
+        return int(np.frombuffer(self.token.download(4), np.uint32)[0])
+
+    def last_logits(self) -> np.ndarray:
+        return np.frombuffer(self.logits.download(), np.float32).copy()
+
+    def cache(self, layer: int, which: str) -> np.ndarray:
+        b = self.prog.by_name[f"cache.{layer}.{which}"]
+        return np.frombuffer(self.bind[b.name].download(), np.uint16).reshape(b.shape).copy()

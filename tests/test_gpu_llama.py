@@ -1,0 +1,60 @@
+"""The Llama-3.2 decode step on the GPU against the oracle: greedy ids identical, logits close."""
+import numpy as np
+import pytest
+
+from sanic_amd import configs
+from sanic_amd.llama import LlamaMachine
+from tests.llama_ref import OracleModel, synth_weights, _upload
+from tests.test_cpu_llama_oracle import TINY
+from tests.util import max_rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _machine(dev, shape, w):
+    bufs = {name: _upload(dev, a) for name, a in w.items()}
+    return LlamaMachine(dev, bufs, shape)
+
+
+def test_tiny_llama_greedy_matches_oracle(dev):
+    w = synth_weights(TINY, seed=5)
+    m = _machine(dev, TINY, w)
+    om = OracleModel(TINY, w)
+    prompt = [3, 17, 250, 9, 44]
+    for pos, t in enumerate(prompt):
+        m.step(t)
+        tok, logits = om.step(t, pos)
+        assert m.last_token() == tok
+        assert max_rel_err(m.last_logits(), logits) < 1e-4
+    for pos in range(len(prompt), TINY.capacity):
+        m.step()
+        tok, logits = om.step(tok, pos)
+        assert m.last_token() == tok, pos
+        assert max_rel_err(m.last_logits(), logits) < 1e-4
+    assert m.position() == TINY.capacity
+
+
+@pytest.fixture(scope="module")
+def full_model(dev):
+    w = synth_weights(configs.LLAMA_1B, seed=11)
+    return w, _machine(dev, configs.LLAMA_1B, w)
+
+
+def test_llama_1b_short_prompt_greedy_ids(full_model):
+    """Full architecture: 6 prompt tokens then 6 greedy steps, ids identical to the oracle."""
+    w, m = full_model
+    om = OracleModel(configs.LLAMA_1B, w)
+    prompt = [128000, 791, 6864, 315, 9822, 374]
+    worst = 0.0
+    for pos, t in enumerate(prompt):
+        m.step(t)
+        tok, logits = om.step(t, pos)
+        worst = max(worst, max_rel_err(m.last_logits(), logits))
+        assert m.last_token() == tok
+    for pos in range(len(prompt), len(prompt) + 6):
+        m.step()
+        tok, logits = om.step(tok, pos)
+        worst = max(worst, max_rel_err(m.last_logits(), logits))
+        assert m.last_token() == tok
+    print("logits max rel err", worst)
+    assert worst < 1e-3

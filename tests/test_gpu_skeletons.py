@@ -1,0 +1,72 @@
+"""Hand-written skeletons on the GPU against the oracle, at the configurations' full sizes."""
+import numpy as np
+import pytest
+
+import oracle
+from sanic_amd import configs, ir
+from sanic_amd.backend import from_bf16_bits
+from tests.util import max_rel_err, run_on_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def bf16_rel(got, want) -> float:
+    """bf16-storage metric of the reference: |g − e| / max(|e|, 1e-3) (tests/metal.rs:2098-2110)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-3)))
+
+
+def _bf16_vals(seed, n, mean=0.0, std=1.0, kind="normal"):
+    return oracle.synth(seed, n, kind, mean, std, dtype=ir.BF16)
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_b1_rmsnorm_gemv_rows_layout(dev, M):
+    """Config B1 with the reference's [out, in] weight layout: gemv skeleton, bf16 ≤ 2e-2."""
+    K, N = 2048, 8192
+    prog = configs.rmsnorm_projection(M=M, K=K, N=N, kmajor=False)
+    x = _bf16_vals(101, M * K).reshape(M, K)
+    g = _bf16_vals(102, K, 1.0, 0.02)
+    wbits = oracle.synth_bf16(103, N * K, "normal", 0.0, 0.02).reshape(N, K)
+    w = from_bf16_bits(wbits).astype(np.float64)
+    got, exe = run_on_gpu(dev, prog, {"x": x, "g": g, "W": w})
+    want = oracle.rmsnorm_proj(x, g, np.ascontiguousarray(wbits.T), 1e-5)
+    print(exe.stage_kernel(0), bf16_rel(got["y"], want))
+    if M == 1:
+        assert exe.stage_kernel(0).startswith("skeleton:gemv")
+    assert bf16_rel(got["y"], want) < 2e-2
+
+
+def test_d1_int4_gemv(dev):
+    """Config D1: packed uint4 [8192, 2048], group 64, s ~ U(0.001, 0.02), z = 8·s."""
+    M, K, N, G = 1, 2048, 8192, 64
+    prog = configs.int4_matmul(M=M, K=K, N=N, G=G)
+    rng = np.random.default_rng(7)
+    u = rng.integers(0, 16, size=(N, K))
+    s = _bf16_vals(201, N * K // G, 0.001, 0.02, kind="uniform").reshape(N, K // G)
+    z = np.array([oracle.round_bf16(8.0 * v) for v in s.reshape(-1)]).reshape(s.shape)
+    x = _bf16_vals(202, M * K).reshape(M, K)
+    got, exe = run_on_gpu(dev, prog, {"x": x, "Wq": u.reshape(N, K // G, G), "S": s, "Z": z})
+    packed = (u[:, 0::2] | (u[:, 1::2] << 4)).astype(np.uint8)
+    want = oracle.int4_matmul(x, packed, s, z, G)
+    print(exe.stage_kernel(0), bf16_rel(got["y"], want))
+    assert exe.stage_kernel(0).startswith("skeleton:gemv")
+    assert bf16_rel(got["y"], want) < 2e-2
+
+
+@pytest.mark.parametrize("pos", [4095, 1000, 0, 63, 64])
+def test_c3_decode_attention_split(dev, pos):
+    """Config C3: 32 query heads / 8 KV heads, 4096-entry cache, split-K combine."""
+    NH, NKV, HD, CAP = 32, 8, 64, 4096
+    prog = configs.decode_attention(NH, NKV, HD, CAP)
+    q = _bf16_vals(301, NH * HD).reshape(NH, HD)
+    kc = _bf16_vals(302, NKV * CAP * HD).reshape(NKV, CAP, HD)
+    vc = _bf16_vals(303, NKV * HD * CAP).reshape(NKV, HD, CAP)
+    got, exe = run_on_gpu(dev, prog, {"q": q, "k_cache": kc, "v_cache": vc, "position": np.array(float(pos))})
+    invf = oracle.inv_freq(500000.0, HD // 2)
+    qr = oracle.rope(q[:, None, :], pos, invf)
+    want = oracle.attention(qr, kc, vc, 1.0 / 8.0, mask=3, q_pos0=pos, v_transposed=True)[:, 0, :]
+    print(exe.stage_kernel(0), pos, bf16_rel(got["o"], want))
+    assert exe.stage_kernel(0).startswith("skeleton:attn_decode")
+    assert bf16_rel(got["o"], want) < 2e-2
