@@ -1,0 +1,175 @@
+"""Headline benchmark: Llama-3.2-1B-shape bf16 decode tokens/s on one MI355X.
+
+Workload (BASELINE.json config E): 16 layers, hidden 2048, 32/8 heads, head_dim 64, SwiGLU 8192,
+vocab 128256, tied embeddings, RoPE θ 5e5 (llama-3 schedule), RMSNorm eps 1e-5; bf16 weights
+N(0, 0.02) (norm gains 1) generated on the device from a seed; a 2048-token random-id prompt is
+prefilled token by token into the in-place bf16 KV cache, then greedy decode steps run as
+back-to-back hipGraph replays (token fed back and position advanced on the device). A step is
+one decode step; `value` = decode tokens/s over the K timed steps (positions 2048 … 2048+K−1).
+
+Also reported: the roofline of the dominant kernel (the batched gate/up norm-fused GEMV, timed
+live with HIP events over back-to-back graph replays of that kernel alone) and the CPU baseline
+(the C restatement of the reference's interpreter semantics timed on this host, rank 0 only).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import struct
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PROMPT = 2048
+HBM_PEAK = 8.0e12
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def device_weights(dev, shape, seed=1234):
+    """bf16 N(0, 0.02) weights (norm gains 1) made on the GPU by torch, bound zero-copy."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    keep, bufs = [], {}
+    for name, shp in shape.weight_shapes():
+        if name.endswith("norm.weight"):
+            t = torch.ones(shp, dtype=torch.bfloat16, device="cuda")
+        else:
+            t = (torch.randn(shp, generator=g, device="cuda", dtype=torch.float32) * 0.02).to(torch.bfloat16)
+        keep.append(t)
+        bufs[name] = dev.wrap(t.data_ptr(), t.numel() * 2)
+    torch.cuda.synchronize()
+    return bufs, keep
+
+
+def dominant_kernel_roofline(dev, shape, weights, reps=50):
+    """Replay the gate/up norm-fused GEMV (one launch, N = 2·ffn, K = hidden) back to back in a
+    hipGraph and time it with HIP events on the library's stream."""
+    from sanic_amd import carrier as C
+    from sanic_amd import ir
+    from sanic_amd.program import STREAM, Program
+    H, F = shape.hidden, shape.ffn
+    p = Program()
+    x = p.input("x", (H,), ir.F32)
+    g = p.input("g", (H,), ir.BF16)
+    for nm in ("gate", "up"):
+        w = p.input(f"W{nm}", (F, H), ir.BF16)
+        p.fused(nm, (F,), H, [(x, (STREAM,)), (g, (STREAM,)), (w, (0, STREAM))],
+                C.norm_fused_projection(H, shape.eps), ir.F32)
+    exe = dev.prepare(p)
+    xb = dev.from_values([0.5] * H, ir.F32)
+    pre = "model.layers.0."
+    binds = {"x": xb, "g": weights[pre + "post_attention_layernorm.weight"],
+             "Wgate": weights[pre + "mlp.gate_proj.weight"], "Wup": weights[pre + "mlp.up_proj.weight"]}
+    rp = exe.capture(binds)
+    rp.step_many(5)
+    secs = rp.step_many(reps) / reps
+    nbytes = 2 * F * H * 2 + H * 4 + H * 2 + 2 * F * 4
+    kname = exe.stage_kernel(0)
+    return {"bound": "hbm", "achieved": nbytes / secs / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": nbytes / secs / HBM_PEAK, "traffic": None,
+            "kernel": f"sanic_gemv_{2 * F}x{H} ({kname})", "bytes_per_launch": nbytes,
+            "us_per_launch": secs * 1e6}
+
+
+def cpu_baseline(shape, seconds_budget=20.0):
+    """The oracle's fused f64 decode step (oracle_llama_step) on this host at position 2048."""
+    import ctypes
+    import numpy as np
+    import oracle
+    from tests.llama_ref import OracleModel, synth_weights
+    threads = oracle.threads()
+    w = synth_weights(shape, seed=99)
+    om = OracleModel(shape, w)
+    n, t0 = 0, time.perf_counter()
+    tok = 1
+    while True:
+        tok, _ = om.step(tok, PROMPT + n)
+        n += 1
+        el = time.perf_counter() - t0
+        if el > seconds_budget / 4 or n >= 8:
+            break
+    return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} decode steps of the full model at positions {PROMPT}..{PROMPT + n - 1} "
+                      f"(f64 fused loops over bf16 weights, {threads} threads, "
+                      f"{os.uname().nodename})"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
+                                   "(see the sharding design note)", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+    from sanic_amd import configs
+    from sanic_amd.backend import HipDevice
+    from sanic_amd.llama import LlamaMachine
+
+    cap = PROMPT + max(32, args.steps, args.warmup)
+    shape = configs.LlamaShape(capacity=cap)
+    torch.cuda.init()
+    dev = HipDevice(0)
+    t0 = time.perf_counter()
+    weights, keep = device_weights(dev, shape)
+    m = LlamaMachine(dev, weights, shape)
+    log(f"prepared in {time.perf_counter() - t0:.1f}s")
+
+    import numpy as np
+    rng = np.random.default_rng(2048)
+    prompt = rng.integers(0, shape.vocab, size=PROMPT).tolist()
+    t0 = time.perf_counter()
+    first = m.prefill(prompt)
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill {PROMPT} tokens token-by-token in {prefill_s:.2f}s; next token {first}")
+
+    # warmup decode steps, then rewind to the end of the prompt and time K steps
+    m.decode(args.warmup)
+    m.set_position(PROMPT)
+    m.set_token(first)
+    dev.sync()
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    gpu_s = m.decode(args.steps)
+    dev.sync()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    elapsed = max(wall, gpu_s)
+    tok_s = args.steps / elapsed
+    ms = elapsed / args.steps * 1e3
+
+    kv_bytes = sum(32768 * (p + 1) for p in range(PROMPT, PROMPT + args.steps)) / args.steps
+    step_bytes = shape.weight_bytes() + kv_bytes
+    roof = dominant_kernel_roofline(dev, shape, weights)
+    step_roof = {"bytes_per_step": step_bytes, "achieved_GBps": step_bytes / (ms * 1e-3) / 1e9,
+                 "frac_of_8TBps": step_bytes / (ms * 1e-3) / HBM_PEAK}
+    cpu = None if args.no_cpu else cpu_baseline(shape)
+    out = {
+        "metric": "tok/s Llama-3.2-1B-shape bf16 decode", "value": tok_s, "unit": "tok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) bf16 weights, random prompt ids)",
+        "config": {"workload": "llama3.2-1b-shape decode, 2048-token prompt prefilled token-by-token, "
+                               f"greedy steps at positions {PROMPT}..{PROMPT + args.steps - 1}",
+                   "global_batch": 1, "seq_len": PROMPT, "parallelism": "single-gpu"},
+        "roofline": roof, "step_roofline": step_roof, "cpu_baseline": cpu,
+        "gpu_event_seconds": gpu_s, "wall_seconds": wall,
+        "prefill_token_by_token_tok_s": PROMPT / prefill_s,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -34,6 +34,9 @@ def precompile_all() -> None:
     """Fill the code-object cache with every shipped configuration's kernels."""
     for s in (None, Sched(lane_stream=True, waves=1), Sched(lane_stream=True, waves=2, split=4)):
         direct_attention(sched=s).precompile()
+    for p in (rmsnorm_projection(kmajor=False), rmsnorm_projection(kmajor=True), int4_matmul(),
+              decode_attention(), llama_decode()):
+        p.precompile()
 
 
 def rmsnorm_projection(M: int = 1, K: int = 2048, N: int = 8192, eps: float = 1e-5,

@@ -484,16 +484,18 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     }
     m.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v));
 
+    const std::string tag = "h" + std::to_string(NH) + "_t" + std::to_string(T);
+    const std::string kpart = "sanic_attn_decode_" + tag, kmerge = "sanic_attn_merge_" + tag;
     std::ostringstream src;
     src << kPrelude << R.args_struct({"float* __restrict__ scratch"});
-    src << "extern \"C\" __global__ void __launch_bounds__(256) sanic_attn_decode(Args a) {\n" << k.str() << "}\n";
-    src << "extern \"C\" __global__ void __launch_bounds__(256) sanic_attn_merge(Args a) {\n" << m.str() << "}\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << kpart << "(Args a) {\n" << k.str() << "}\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << kmerge << "(Args a) {\n" << m.str() << "}\n";
     out.kernel_kind = "skeleton:attn_decode[rep " + std::to_string(REP) + "]";
     out.source = src.str();
     std::vector<Arg> args = R.arg_list();
     args.push_back({Arg::SCRATCH, part_off});
-    out.launches.push_back({"sanic_attn_decode", "", dim3((unsigned)NG, (unsigned)NCH), dim3(256), 0, args});
-    out.launches.push_back({"sanic_attn_merge", "", dim3((unsigned)((gvol + 255) / 256)), dim3(256), 0, args});
+    out.launches.push_back({kpart, "", dim3((unsigned)NG, (unsigned)NCH), dim3(256), 0, args});
+    out.launches.push_back({kmerge, "", dim3((unsigned)((gvol + 255) / 256)), dim3(256), 0, args});
     return true;
 }
 

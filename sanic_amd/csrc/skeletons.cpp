@@ -595,8 +595,10 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t&, std::vector
     k.indent--;
     k.line("}");
 
+    // kernel names carry the shape so profiles tell the launches apart
+    const std::string kname = "sanic_gemv_" + std::to_string(NTOT) + "x" + std::to_string(K);
     std::ostringstream src;
-    src << kPrelude << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(256) sanic_gemv(Args a) {\n"
+    src << kPrelude << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n"
         << k.str() << "}\n";
     int64_t waves = (NTOT + RQ - 1) / RQ;
     int64_t blocks = std::min<int64_t>((waves + 3) / 4, 2048);
@@ -604,7 +606,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t&, std::vector
     L.kernel_kind = "skeleton:gemv" + std::string(group.size() > 1 ? "[batched " + std::to_string(group.size()) + "]" : "");
     L.source = src.str();
     uint32_t lds = (uint32_t)((SC * K + 4 * std::max(SR, 1)) * 4);
-    L.launches.push_back({"sanic_gemv", "", dim3((unsigned)blocks), dim3(256), lds, R.arg_list()});
+    L.launches.push_back({kname, "", dim3((unsigned)blocks), dim3(256), lds, R.arg_list()});
     out.push_back(std::move(L));
     for (size_t g = 1; g < group.size(); g++) {
         LoweredStage B;

@@ -57,4 +57,6 @@ def test_llama_1b_short_prompt_greedy_ids(full_model):
         worst = max(worst, max_rel_err(m.last_logits(), logits))
         assert m.last_token() == tok
     print("logits max rel err", worst)
-    assert worst < 1e-3
+    # logits are f32 but sit downstream of the bf16 K/V cache: an f32-vs-f64 difference can flip
+    # one bf16 rounding of a cache entry (2^-8 relative), so the bf16 bound applies here
+    assert worst < 2e-2
