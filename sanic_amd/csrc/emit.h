@@ -60,7 +60,9 @@ void emit_window(Renderer& R, Code& code, const sanic_stage& st, const std::vect
 int64_t dtype_bytes(int dt, int64_t n);
 void validate(const sanic_program_desc* d);
 
-LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& scratch);
+LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& scratch, const std::vector<int>& tails);
+bool tail_candidate(const sanic_program_desc* d, int si);
+void emit_pointwise_loop(Renderer& R, Code& body, const sanic_program_desc* d, int si, const std::string& tid, int nth);
 LoweredStage lower_pointwise(const sanic_program_desc* d, int si);
 // Offer a stage to the hand-written skeletons; false when none accepts its structure.
 bool lower_skeleton(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out);

@@ -242,6 +242,8 @@ std::string flit(double v) {
 
 const char* kPrelude = R"PRE(
 typedef long long idx_t;
+typedef unsigned sanic_u32x4 __attribute__((ext_vector_type(4)));
+typedef float sanic_f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float sanic_bf16(unsigned short b) { return __uint_as_float(((unsigned)b) << 16); }
 __device__ __forceinline__ unsigned short sanic_to_bf16(float v) {
   unsigned b = __float_as_uint(v);
@@ -753,7 +755,7 @@ static void emit_finish(Renderer& R, Code& code, const sanic_stage& st, const st
     code.line(store_stmt(R.param(st.out_buffer), gid, st.out_dtype, v));
 }
 
-LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& scratch) {
+LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& scratch, const std::vector<int>& tails) {
     const sanic_stage& st = d->stages[si];
     const sanic_carrier& c = st.carrier;
     LoweredStage L;
@@ -798,7 +800,9 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     int nw = nth / 64;
     L.kernel_kind = split > 1 ? "fold:split" : "fold:coop";
     int64_t part_off = scratch;
-    if (split > 1) scratch += ((gvol * split * c.slots * 4 + 255) / 256) * 256;
+    const bool fused_merge = split > 1 && gvol <= 4096;
+    const int64_t part_bytes = ((gvol * split * c.slots * 4 + 255) / 256) * 256;
+    if (split > 1) scratch += part_bytes + (fused_merge ? 256 : 0);
     body.line("const idx_t gid = (idx_t)blockIdx.x / " + std::to_string(split) + ";");
     body.line("const int part = (int)(blockIdx.x % " + std::to_string(split) + ");");
     body.line("const int t = threadIdx.x, lane = t & 63, wv = t >> 6;");
@@ -846,7 +850,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
         for (int k = 0; k < c.slots; k++) body.line("  lds_acc[wv][" + std::to_string(k) + "] = acc" + std::to_string(k) + ";");
         body.line("}");
         body.line("__syncthreads();");
-        body.line("if (t != 0) return;");
+        body.line(fused_merge ? "if (t == 0) {" : "if (t != 0) return;");
         body.line("for (int w = 1; w < " + std::to_string(nw) + "; ++w) {");
         body.indent++;
         for (int k = 0; k < c.slots; k++)
@@ -855,7 +859,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
         body.indent--;
         body.line("}");
     } else {
-        body.line("if (t != 0) return;");
+        body.line(fused_merge ? "if (t == 0) {" : "if (t != 0) return;");
     }
     if (split == 1) {
         emit_finish(R, body, st, "gid");
@@ -866,10 +870,56 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
         L.source = src.str();
         return L;
     }
-    // split: write the partial carrier, then a second kernel merges with the combine
+    // split: write the partial carrier, then merge with the combine: in the last workgroup to
+    // arrive when the grid is small (then the following small pointwise stages run there too),
+    // else in a second kernel
     for (int k = 0; k < c.slots; k++)
         body.line("a.scratch[((idx_t)gid * " + std::to_string(split) + " + part) * " + std::to_string(c.slots) + " + " +
                   std::to_string(k) + "] = acc" + std::to_string(k) + ";");
+    auto merge_point = [&](Renderer& RR, Code& mb) {
+        decode_grid(mb, st, "gid");
+        mb.line("const float* pp = a.scratch + (idx_t)gid * " + std::to_string(split * c.slots) + ";");
+        for (int k = 0; k < c.slots; k++) mb.line("float acc" + std::to_string(k) + " = pp[" + std::to_string(k) + "];");
+        mb.line("for (int p = 1; p < " + std::to_string(split) + "; ++p) {");
+        mb.indent++;
+        for (int k = 0; k < c.slots; k++)
+            mb.line("const float o" + std::to_string(k) + " = pp[p * " + std::to_string(c.slots) + " + " + std::to_string(k) + "];");
+        emit_merge(RR, mb, c, "o");
+        mb.indent--;
+        mb.line("}");
+        emit_finish(RR, mb, st, "gid");
+    };
+    if (fused_merge) {
+        body.line("}");
+        body.line("__shared__ int sanic_last;");
+        body.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(part_bytes) + ");");
+        body.line("__threadfence();");
+        body.line("__syncthreads();");
+        body.line("if (t == 0) sanic_last = atomicAdd(cnt, 1u) == gridDim.x - 1;");
+        body.line("__syncthreads();");
+        body.line("if (!sanic_last) return;");
+        body.line("__threadfence();");
+        body.line("for (idx_t gid = t; gid < " + std::to_string(gvol) + "; gid += " + std::to_string(nth) + ") {");
+        body.indent++;
+        R.memo.emplace_back();
+        merge_point(R, body);
+        R.memo.pop_back();
+        body.indent--;
+        body.line("}");
+        for (int ts : tails) {
+            body.line("__threadfence(); __syncthreads();");
+            emit_pointwise_loop(R, body, d, ts, "(idx_t)t", nth);
+        }
+        body.line("if (t == 0) *cnt = 0u;");
+        src << R.args_struct({"float* __restrict__ scratch"});
+        src << "extern \"C\" __global__ void __launch_bounds__(" << nth << ") sanic_fold_split(Args a) {\n" << body.str() << "}\n";
+        std::vector<Arg> args = R.arg_list();
+        args.push_back({Arg::SCRATCH, part_off});
+        L.launches.push_back({"sanic_fold_split", "", dim3((unsigned)(gvol * split)), dim3(nth), 0, args});
+        L.kernel_kind = "fold:split+merge" + std::string(tails.empty() ? "" : "+tail" + std::to_string(tails.size()));
+        L.source = src.str();
+        return L;
+    }
     Code mb;
     mb.indent = 1;
     Renderer R2(d);
@@ -877,17 +927,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     R2.buf_param = R.buf_param;
     mb.line("const idx_t gid = (idx_t)blockIdx.x * 256 + threadIdx.x;");
     mb.line("if (gid >= " + std::to_string(gvol) + ") return;");
-    decode_grid(mb, st, "gid");
-    mb.line("const float* pp = a.scratch + (idx_t)gid * " + std::to_string(split * c.slots) + ";");
-    for (int k = 0; k < c.slots; k++) mb.line("float acc" + std::to_string(k) + " = pp[" + std::to_string(k) + "];");
-    mb.line("for (int p = 1; p < " + std::to_string(split) + "; ++p) {");
-    mb.indent++;
-    for (int k = 0; k < c.slots; k++)
-        mb.line("const float o" + std::to_string(k) + " = pp[p * " + std::to_string(c.slots) + " + " + std::to_string(k) + "];");
-    emit_merge(R2, mb, c, "o");
-    mb.indent--;
-    mb.line("}");
-    emit_finish(R2, mb, st, "gid");
+    merge_point(R2, mb);
     // both kernels share one Args layout: the union of their buffers
     for (int b : R2.bufs) R.param(b);
     src << R.args_struct({"float* __restrict__ scratch"});
@@ -948,9 +988,26 @@ Lowered lower_program(const sanic_program_desc* d) {
                 continue;
             }
             LoweredStage L;
-            if (getenv("SANIC_HIP_GENERIC") || !lower_skeleton(d, s, out.scratch_bytes, L))
-                L = lower_generic_fold(d, s, out.scratch_bytes);
+            if (!getenv("SANIC_HIP_GENERIC") && lower_skeleton(d, s, out.scratch_bytes, L)) {
+                out.stages.push_back(std::move(L));
+                s++;
+                continue;
+            }
+            // a small split fold merges in its last workgroup and runs the small pointwise
+            // stages that follow it there as well
+            std::vector<int> tails;
+            int64_t gv = 1;
+            for (int j = 0; j < st.rank; j++) gv *= st.grid[j];
+            if (st.sched.lane_stream && st.sched.split > 1 && std::min<int64_t>(st.sched.split, st.stream) > 1 && gv <= 4096)
+                for (int t = s + 1; tail_candidate(d, t) && tails.size() < 4; t++) tails.push_back(t);
+            L = lower_generic_fold(d, s, out.scratch_bytes, tails);
             out.stages.push_back(std::move(L));
+            for (size_t t = 0; t < tails.size(); t++) {
+                LoweredStage B;
+                B.kernel_kind = "tail-of:" + std::to_string(s);
+                out.stages.push_back(std::move(B));
+            }
+            s += (int)tails.size();
         } else {
             LoweredStage L;
             if (getenv("SANIC_HIP_GENERIC") || !lower_pointwise_skeleton(d, s, out.scratch_bytes, L))

@@ -407,6 +407,9 @@ static void bind_all(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int 
         }
     }
     scratch.reset(new_buffer(exe->dev, (size_t)std::max<int64_t>(exe->low.scratch_bytes, 256)));
+    // arrival counters in the arena must start at zero; kernels re-arm them after each launch
+    SANIC_HIP(hipMemsetAsync(scratch->ptr(), 0, scratch->bytes, exe->dev->stream));
+    SANIC_HIP(hipStreamSynchronize(exe->dev->stream));
 }
 
 int sanic_hip_execute(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int n_bindings, sanic_hip_buffer** outputs) {

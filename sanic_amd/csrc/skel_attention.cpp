@@ -272,15 +272,14 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("}");
     }
     k.line("const idx_t t0 = lo0 + chunk * " + std::to_string(CH) + ";");
-    k.line("float* part = a.scratch + (chunk * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + ") * " + std::to_string(PSZ) + ";");
+    k.line("float* part = a.scratch + " + std::to_string(part_off / 4) + " + (chunk * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + ") * " + std::to_string(PSZ) + ";");
     // identity partial for chunks past the visible window
     k.line("if (t0 >= hi0) {");
     k.line("  for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += 256) {");
     k.line("    const int r = i / " + std::to_string(PSZ) + ", f = i % " + std::to_string(PSZ) + ";");
     k.line("    part[r * " + std::to_string(PSZ) + " + f] = f == 0 ? " + flit(c.identity[P.max_slot]) + " : 0.0f;");
     k.line("  }");
-    k.line("  return;");
-    k.line("}");
+    k.line("} else {");
     k.line("const idx_t t1 = t0 + " + std::to_string(CH) + " < hi0 ? t0 + " + std::to_string(CH) + " : hi0;");
     // query vectors (the A side, rendered) into LDS
     k.line("for (int i = tid; i < " + std::to_string(REP * HD) + "; i += 256) {");
@@ -437,65 +436,101 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.indent--;
     k.line("}");
 
-    // merge kernel: one lane per output point
-    Code m;
-    m.indent = 1;
-    int64_t gvol = 1;
-    for (int j = 0; j < st.rank; j++) gvol *= st.grid[j];
-    m.line("const idx_t gid = (idx_t)blockIdx.x * 256 + threadIdx.x;");
-    m.line("if (gid >= " + std::to_string(gvol) + ") return;");
-    decode_grid(m, st, "gid");
-    std::string hexpr = P.hdim >= 0 ? "g" + std::to_string(P.hdim) : "0";
-    std::string eexpr = "g" + std::to_string(P.edim);
-    // slot -> partial field
+    k.line("}  // visible chunk");
+    // Merge, fused: the last workgroup of this KV group to finish stages the group's partials in
+    // LDS and folds them per output point with the carrier's rendered combine (program order is
+    // that of run_carrier_split: chunk 0 first), then projects, runs the epilogue and stores.
+    int64_t counter_off = scratch;
+    scratch += ((NG * 4 + 255) / 256) * 256;
+    const int64_t GP = NCH * REP * PSZ;       // floats of one group's partials
+    const bool in_lds = GP * 4 <= 48 * 1024;
+    k.line("{");
+    k.indent++;
+    k.line("__shared__ int sanic_last;");
+    k.line("__threadfence();");
+    k.line("__syncthreads();");
+    k.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(counter_off) + ") + grp;");
+    k.line("if (tid == 0) sanic_last = atomicAdd(cnt, 1u) == " + std::to_string(NCH) + "u - 1u;");
+    k.line("__syncthreads();");
+    k.line("if (!sanic_last) return;");
+    k.line("__threadfence();");
+    std::string src_expr;   // partial (chunk ch, head-in-group r, field f)
+    if (in_lds) {
+        k.line("__shared__ float g_lds[" + std::to_string(GP) + "];");
+        k.line("for (int i = tid; i < " + std::to_string(GP) + "; i += 256) {");
+        k.line("  const int ch = i / " + std::to_string(REP * PSZ) + ", rem = i % " + std::to_string(REP * PSZ) + ";");
+        k.line("  g_lds[i] = a.scratch[" + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + ") * " + std::to_string(PSZ) + " + rem];");
+        k.line("}");
+        k.line("__syncthreads();");
+        src_expr = "g_lds[(ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + " + FIELD]";
+    } else {
+        src_expr = "a.scratch[" + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + " + FIELD]";
+    }
+    k.line("if (tid == 0) *cnt = 0u;");
+    k.line("for (int pt = tid; pt < " + std::to_string(REP * E) + "; pt += 256) {");
+    k.indent++;
+    k.line("const int r = pt / " + std::to_string(E) + ", ee = pt % " + std::to_string(E) + ";");
+    // grid coordinates of this output point
+    for (int j = 0; j < st.rank; j++) {
+        std::string v = j == P.hdim ? "(grp * " + std::to_string(REP) + " + r)" : j == P.edim ? "(idx_t)ee" : "0";
+        k.line("const idx_t g" + std::to_string(j) + " = " + v + ";");
+    }
+    std::string lin = "0";
+    for (int j = 0; j < st.rank; j++)
+        lin = j == 0 ? "g0" : "(" + lin + " * " + std::to_string(st.grid[j]) + " + g" + std::to_string(j) + ")";
+    k.line("const idx_t gid = " + lin + ";");
     auto field = [&](int slot) -> std::string {
         if (slot == P.max_slot) return "0";
-        for (int s = 0; s < NS; s++) if (P.scalar_slots[s] == slot) return std::to_string(1 + s);
-        for (int v = 0; v < NV; v++) if (P.vec_slots[v] == slot) return std::to_string(1 + NS + v * E) + " + " + eexpr;
+        for (int sidx = 0; sidx < NS; sidx++) if (P.scalar_slots[sidx] == slot) return std::to_string(1 + sidx);
+        for (int v = 0; v < NV; v++) if (P.vec_slots[v] == slot) return std::to_string(1 + NS + v * E) + " + ee";
         return "0";
     };
-    m.line("const float* pp = a.scratch + " + hexpr + " * " + std::to_string(PSZ) + ";");
-    for (int s = 0; s < c.slots; s++) m.line("float acc" + std::to_string(s) + " = pp[" + field(s) + "];");
-    m.line("for (idx_t ch = 1; ch < " + std::to_string(NCH) + "; ++ch) {");
-    m.indent++;
-    m.line("const float* q = pp + ch * " + std::to_string(NH * PSZ) + ";");
-    for (int s = 0; s < c.slots; s++) m.line("const float o" + std::to_string(s) + " = q[" + field(s) + "];");
-    m.line("{");
-    m.indent++;
-    for (int s = 0; s < c.slots; s++) {
-        std::string v = R.expr(m, c.combine[s], "", "acc", "o", "");
-        m.line("const float nx" + std::to_string(s) + " = " + v + ";");
+    auto at = [&](const std::string& ch, int slot) {
+        std::string e = src_expr;
+        e.replace(e.find("ch *"), 2, ch);
+        e.replace(e.find("FIELD"), 5, field(slot));
+        return e;
+    };
+    for (int sidx = 0; sidx < c.slots; sidx++) k.line("float acc" + std::to_string(sidx) + " = " + at("0", sidx) + ";");
+    k.line("for (int ch = 1; ch < " + std::to_string(NCH) + "; ++ch) {");
+    k.indent++;
+    for (int sidx = 0; sidx < c.slots; sidx++) k.line("const float o" + std::to_string(sidx) + " = " + at("ch", sidx) + ";");
+    R.memo.emplace_back();
+    for (int sidx = 0; sidx < c.slots; sidx++) {
+        std::string v = R.expr(k, c.combine[sidx], "", "acc", "o", "");
+        k.line("const float nx" + std::to_string(sidx) + " = " + v + ";");
     }
-    for (int s = 0; s < c.slots; s++) m.line("acc" + std::to_string(s) + " = nx" + std::to_string(s) + ";");
-    m.indent--;
-    m.line("}");
-    m.indent--;
-    m.line("}");
-    std::string f = R.expr(m, c.project, "", "", "", "acc");
-    m.line("const float fold_v = " + f + ";");
+    R.memo.pop_back();
+    for (int sidx = 0; sidx < c.slots; sidx++) k.line("acc" + std::to_string(sidx) + " = nx" + std::to_string(sidx) + ";");
+    k.indent--;
+    k.line("}");
+    R.memo.emplace_back();
+    std::string f = R.expr(k, c.project, "", "", "", "acc");
+    k.line("const float fold_v = " + f + ";");
     std::string v = "fold_v";
     if (st.epilogue >= 0) {
         std::vector<std::string> gc;
         for (int j = 0; j < st.rank; j++) gc.push_back("g" + std::to_string(j));
         R.fold_var = "fold_v";
-        R.memo.emplace_back();
-        v = R.value(m, st.epilogue, gc);
-        R.memo.pop_back();
+        v = R.value(k, st.epilogue, gc);
     }
-    m.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v));
+    R.memo.pop_back();
+    k.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v));
+    k.indent--;
+    k.line("}");
+    k.indent--;
+    k.line("}");
 
     const std::string tag = "h" + std::to_string(NH) + "_t" + std::to_string(T);
-    const std::string kpart = "sanic_attn_decode_" + tag, kmerge = "sanic_attn_merge_" + tag;
+    const std::string kpart = "sanic_attn_decode_" + tag;
     std::ostringstream src;
     src << kPrelude << R.args_struct({"float* __restrict__ scratch"});
     src << "extern \"C\" __global__ void __launch_bounds__(256) " << kpart << "(Args a) {\n" << k.str() << "}\n";
-    src << "extern \"C\" __global__ void __launch_bounds__(256) " << kmerge << "(Args a) {\n" << m.str() << "}\n";
     out.kernel_kind = "skeleton:attn_decode[rep " + std::to_string(REP) + "]";
     out.source = src.str();
     std::vector<Arg> args = R.arg_list();
-    args.push_back({Arg::SCRATCH, part_off});
+    args.push_back({Arg::SCRATCH, 0});
     out.launches.push_back({kpart, "", dim3((unsigned)NG, (unsigned)NCH), dim3(256), 0, args});
-    out.launches.push_back({kmerge, "", dim3((unsigned)((gvol + 255) / 256)), dim3(256), 0, args});
     return true;
 }
 

@@ -48,3 +48,23 @@ def test_reduce_rows_known_answer(dev):
     p.fused("Y", (2,), 2, [(x, (0, STREAM))], C.plain(ir.M_ADD))
     got, _ = run_on_gpu(dev, p, {"X": np.array([[1.0, 2.0], [3.0, 4.0]])})
     assert got["Y"].tolist() == [3.0, 7.0]
+
+
+def test_split_fold_merges_in_last_workgroup(dev):
+    """A small split fold (argmax key/tie carrier over 100k elements, 64 workgroups) merges in
+    its last-arriving workgroup and matches the first-maximum index exactly, twice in a row
+    (the arrival counter re-arms itself)."""
+    n = 100_000
+    p = Program()
+    x = p.input("X", (n,))
+    p.fused("I", (1,), n, [(x, (STREAM,)), (ir.iota(n), (STREAM,))], C.first_argmax(), ir.U32,
+            sched=Sched(lane_stream=True, waves=4, chunk=4, split=64))
+    vals = oracle.lcg(99, n)
+    vals[77_777] = 5.0
+    vals[88_888] = 5.0          # a tie: the first index wins
+    exe = dev.prepare(p)
+    assert exe.stage_kernel(0).startswith("fold:split+merge")
+    buf = dev.from_values(vals, ir.F32)
+    for _ in range(2):
+        out = exe.execute({"X": buf})["I"].read(ir.U32, 1)
+        assert int(out[0]) == 77_777
