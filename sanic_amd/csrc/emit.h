@@ -2,6 +2,7 @@
 // (emit_hip.cpp) and the hand-written skeletons (skeletons.cpp).
 #pragma once
 #include <map>
+#include <set>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -25,7 +26,8 @@ struct Renderer {
     std::vector<std::map<std::string, std::string>> memo;  // scoped common-subexpression cache
     int tmp = 0;
     std::string fold_var = "fold_v";
-    std::map<int, std::string> subst;            // node id -> precomputed value expression
+    std::map<int, std::string> subst;
+    std::set<int> coherent;                      // buffers read with device-coherent loads            // node id -> precomputed value expression
     explicit Renderer(const sanic_program_desc* dd) : d(dd) { memo.emplace_back(); }
 
     std::string param(int buffer);
@@ -50,7 +52,7 @@ const char* ctype_of(int dt);
 std::string map_expr(int op, const std::string& a, const std::string& b, const std::string& c);
 std::string monoid_combine(int m, const std::string& a, const std::string& b);
 double monoid_identity(int m);
-std::string store_stmt(const std::string& ptr, const std::string& idx, int dt, const std::string& v);
+std::string store_stmt(const std::string& ptr, const std::string& idx, int dt, const std::string& v, bool coherent = false);
 void decode_grid(Code& code, const sanic_stage& st, const std::string& gid);
 std::vector<std::string> leaf_coords(const sanic_stage& st, const sanic_program_desc* d, int l,
                                      const std::string& s);

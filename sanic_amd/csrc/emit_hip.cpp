@@ -262,6 +262,14 @@ __device__ __forceinline__ float sanic_w4(const unsigned char* p, idx_t i) {
 __device__ __forceinline__ float sanic_u4(const unsigned char* p, idx_t i) {
   return (float)(int)((p[i >> 1] >> ((i & 1) << 2)) & 0xF);
 }
+// device-coherent (agent-scope) accesses for data exchanged between workgroups of one kernel:
+// written through to the level every XCD sees, read past the local L2
+template <class T> __device__ __forceinline__ T sanic_ld(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T> __device__ __forceinline__ void sanic_st(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ float sanic_lse(float a, float b) {
   if (a == -__builtin_huge_valf()) return b;
   if (b == -__builtin_huge_valf()) return a;
@@ -370,6 +378,14 @@ std::string Renderer::load(int node, const std::vector<std::string>& c) {
     }
     if (lin.empty()) lin = "0";
     std::string p = param(n.buffer);
+    if (coherent.count(n.buffer)) {
+        std::string a = "sanic_ld(" + p + " + " + lin + ")";
+        switch (n.dtype) {
+        case SANIC_F32: return a;
+        case SANIC_BF16: return "sanic_bf16(" + a + ")";
+        case SANIC_F16: case SANIC_U32: case SANIC_I8: return "(float)" + a;
+        }
+    }
     switch (n.dtype) {
     case SANIC_F32: return p + "[" + lin + "]";
     case SANIC_F16: return "(float)" + p + "[" + lin + "]";
@@ -528,12 +544,28 @@ std::string Renderer::expr(Code& code, int e, const std::string& item, const std
     std::string s[3];
     int kids[3] = {x.a, x.b, x.c};
     for (int k = 0; k < 3; k++) if (kids[k] >= 0) s[k] = expr(code, kids[k], item, a, b, f);
+    // structurally equal subexpressions (e.g. the rescale factor every ExpShifted slot of a
+    // carrier shares) are computed once per scope
+    std::string text = map_expr(x.op, s[0], s[1], s[2]);
+    for (auto it = memo.rbegin(); it != memo.rend(); ++it) {
+        auto hit = it->find("expr:" + text);
+        if (hit != it->end()) return hit->second;
+    }
     std::string out = fresh("e");
-    code.line("const float " + out + " = " + map_expr(x.op, s[0], s[1], s[2]) + ";");
+    code.line("const float " + out + " = " + text + ";");
+    memo.back()["expr:" + text] = out;
     return out;
 }
 
-std::string store_stmt(const std::string& ptr, const std::string& idx, int dt, const std::string& v) {
+std::string store_stmt(const std::string& ptr, const std::string& idx, int dt, const std::string& v, bool coherent) {
+    if (coherent) {
+        switch (dt) {
+        case SANIC_F32: return "sanic_st(" + ptr + " + " + idx + ", (float)(" + v + "));";
+        case SANIC_F16: return "sanic_st(" + ptr + " + " + idx + ", (_Float16)(" + v + "));";
+        case SANIC_BF16: return "sanic_st(" + ptr + " + " + idx + ", sanic_to_bf16(" + v + "));";
+        case SANIC_U32: return "sanic_st(" + ptr + " + " + idx + ", sanic_to_u32(" + v + "));";
+        }
+    }
     switch (dt) {
     case SANIC_F32: return ptr + "[" + idx + "] = " + v + ";";
     case SANIC_F16: return ptr + "[" + idx + "] = (_Float16)" + v + ";";
@@ -731,11 +763,13 @@ static void emit_fold_body(Renderer& R, Code& code, const sanic_stage& st, const
 static void emit_merge(Renderer& R, Code& code, const sanic_carrier& c, const std::string& oth) {
     code.line("{");
     code.indent++;
+    R.memo.emplace_back();
     for (int k = 0; k < c.slots; k++) {
         std::string v = R.expr(code, c.combine[k], "", "acc", oth, "");
         code.line("const float nx" + std::to_string(k) + " = " + v + ";");
     }
     for (int k = 0; k < c.slots; k++) code.line("acc" + std::to_string(k) + " = nx" + std::to_string(k) + ";");
+    R.memo.pop_back();
     code.indent--;
     code.line("}");
 }
@@ -873,17 +907,18 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     // split: write the partial carrier, then merge with the combine: in the last workgroup to
     // arrive when the grid is small (then the following small pointwise stages run there too),
     // else in a second kernel
-    for (int k = 0; k < c.slots; k++)
-        body.line("a.scratch[((idx_t)gid * " + std::to_string(split) + " + part) * " + std::to_string(c.slots) + " + " +
-                  std::to_string(k) + "] = acc" + std::to_string(k) + ";");
+    for (int k = 0; k < c.slots; k++) {
+        std::string at = "a.scratch + ((idx_t)gid * " + std::to_string(split) + " + part) * " + std::to_string(c.slots) + " + " + std::to_string(k);
+        body.line(fused_merge ? "sanic_st(" + at + ", acc" + std::to_string(k) + ");" : "*(" + at + ") = acc" + std::to_string(k) + ";");
+    }
     auto merge_point = [&](Renderer& RR, Code& mb) {
         decode_grid(mb, st, "gid");
         mb.line("const float* pp = a.scratch + (idx_t)gid * " + std::to_string(split * c.slots) + ";");
-        for (int k = 0; k < c.slots; k++) mb.line("float acc" + std::to_string(k) + " = pp[" + std::to_string(k) + "];");
+        for (int k = 0; k < c.slots; k++) mb.line("float acc" + std::to_string(k) + " = sanic_ld(pp + " + std::to_string(k) + ");");
         mb.line("for (int p = 1; p < " + std::to_string(split) + "; ++p) {");
         mb.indent++;
         for (int k = 0; k < c.slots; k++)
-            mb.line("const float o" + std::to_string(k) + " = pp[p * " + std::to_string(c.slots) + " + " + std::to_string(k) + "];");
+            mb.line("const float o" + std::to_string(k) + " = sanic_ld(pp + p * " + std::to_string(c.slots) + " + " + std::to_string(k) + ");");
         emit_merge(RR, mb, c, "o");
         mb.indent--;
         mb.line("}");
@@ -893,12 +928,11 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
         body.line("}");
         body.line("__shared__ int sanic_last;");
         body.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(part_bytes) + ");");
-        body.line("__threadfence();");
+        body.line("__builtin_amdgcn_s_waitcnt(0);");
         body.line("__syncthreads();");
-        body.line("if (t == 0) sanic_last = atomicAdd(cnt, 1u) == gridDim.x - 1;");
+        body.line("if (t == 0) sanic_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;");
         body.line("__syncthreads();");
         body.line("if (!sanic_last) return;");
-        body.line("__threadfence();");
         body.line("for (idx_t gid = t; gid < " + std::to_string(gvol) + "; gid += " + std::to_string(nth) + ") {");
         body.indent++;
         R.memo.emplace_back();
@@ -907,10 +941,10 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
         body.indent--;
         body.line("}");
         for (int ts : tails) {
-            body.line("__threadfence(); __syncthreads();");
+            body.line("__syncthreads();");
             emit_pointwise_loop(R, body, d, ts, "(idx_t)t", nth);
         }
-        body.line("if (t == 0) *cnt = 0u;");
+        body.line("if (t == 0) sanic_st(cnt, 0u);");
         src << R.args_struct({"float* __restrict__ scratch"});
         src << "extern \"C\" __global__ void __launch_bounds__(" << nth << ") sanic_fold_split(Args a) {\n" << body.str() << "}\n";
         std::vector<Arg> args = R.arg_list();

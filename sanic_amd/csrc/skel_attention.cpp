@@ -238,7 +238,8 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const int REP = P.rep;
     const int64_t HD = P.dot.depth, E = P.E, T = P.T, NH = P.NH;
     const int64_t NG = NH / REP;
-    const int CH = 64;                            // stream positions per workgroup
+    int CH = 256;                                 // stream positions per workgroup
+    if (const char* e = getenv("SANIC_ATTN_CH")) CH = std::max(64, std::min(1024, atoi(e) / 64 * 64));
     const int64_t NCH = (T + CH - 1) / CH;
     const int NS = (int)P.scalar_slots.size(), NV = (int)P.vec_slots.size();
     const int PSZ = 1 + NS + NV * (int)E;         // floats per (chunk, head) partial
@@ -277,7 +278,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("if (t0 >= hi0) {");
     k.line("  for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += 256) {");
     k.line("    const int r = i / " + std::to_string(PSZ) + ", f = i % " + std::to_string(PSZ) + ";");
-    k.line("    part[r * " + std::to_string(PSZ) + " + f] = f == 0 ? " + flit(c.identity[P.max_slot]) + " : 0.0f;");
+    k.line("    sanic_st(part + r * " + std::to_string(PSZ) + " + f, f == 0 ? " + flit(c.identity[P.max_slot]) + " : 0.0f);");
     k.line("  }");
     k.line("} else {");
     k.line("const idx_t t1 = t0 + " + std::to_string(CH) + " < hi0 ? t0 + " + std::to_string(CH) + " : hi0;");
@@ -303,6 +304,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     addr_parts(P.dot.kacc.addr, repk, NH, kt, kd, kh);
     int64_t kbase = P.dot.kacc.addr.c0;
     k.line("const unsigned short* __restrict__ kp = " + R.param(P.dot.kacc.buffer) + " + " + std::to_string(kbase) + " + grp * " + std::to_string(kh) + ";");
+    k.line("#pragma unroll");
     k.line("for (int pass = 0; pass < " + std::to_string((CH + TPP - 1) / TPP) + "; ++pass) {");
     k.indent++;
     k.line("const int tl = pass * " + std::to_string(TPP) + " + tid / " + std::to_string(LPT) + ";");
@@ -384,11 +386,13 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("const unsigned short* __restrict__ vp = " + R.param(P.vacc.buffer) + " + " + std::to_string(vbase) + " + grp * " + std::to_string(vh) + ";");
     k.line("for (int e = tid % 64; e < " + std::to_string(E) + "; e += 64) {");
     k.indent++;
-    k.line("const int tg = tid / 64;");   // 4 groups of 16 positions
+    k.line("const int tg = tid / 64;");   // 4 groups of CH/4 positions, in runs of 16
     k.line("float o[" + std::to_string(REP) + "];");
     k.line("#pragma unroll");
     k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = 0.0f;");
-    k.line("const int tbase = tg * 16;");
+    k.line("#pragma unroll");
+    k.line("for (int sb = 0; sb < " + std::to_string(CH / 64) + "; ++sb) {");
+    k.line("const int tbase = tg * " + std::to_string(CH / 4) + " + sb * 16;");
     if (vt == 1) {
         k.line("if (t0 + tbase + 16 <= t1) {");
         k.line("  const uint4 va = *(const uint4*)(vp + e * " + std::to_string(ve) + " + t0 + tbase);");
@@ -418,6 +422,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("  }");
         k.line("}");
     }
+    k.line("}");
     k.line("#pragma unroll");
     k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) o_lds[tg][r][e] = o[r];");
     k.indent--;
@@ -432,7 +437,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     for (int s = 0; s < NS; s++)
         k.line("else if (f == " + std::to_string(1 + s) + ") v = " + flit(P.scalar_into[s]) + " * stat_lds[r][1];");
     k.line("else { const int e = (f - " + std::to_string(1 + NS) + ") % " + std::to_string(E) + "; v = ((o_lds[0][r][e] + o_lds[1][r][e]) + o_lds[2][r][e]) + o_lds[3][r][e]; }");
-    k.line("part[r * " + std::to_string(PSZ) + " + f] = v;");
+    k.line("sanic_st(part + r * " + std::to_string(PSZ) + " + f, v);");
     k.indent--;
     k.line("}");
 
@@ -447,26 +452,25 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("{");
     k.indent++;
     k.line("__shared__ int sanic_last;");
-    k.line("__threadfence();");
+    k.line("__builtin_amdgcn_s_waitcnt(0);");
     k.line("__syncthreads();");
     k.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(counter_off) + ") + grp;");
-    k.line("if (tid == 0) sanic_last = atomicAdd(cnt, 1u) == " + std::to_string(NCH) + "u - 1u;");
+    k.line("if (tid == 0) sanic_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == " + std::to_string(NCH) + "u - 1u;");
     k.line("__syncthreads();");
     k.line("if (!sanic_last) return;");
-    k.line("__threadfence();");
     std::string src_expr;   // partial (chunk ch, head-in-group r, field f)
     if (in_lds) {
         k.line("__shared__ float g_lds[" + std::to_string(GP) + "];");
         k.line("for (int i = tid; i < " + std::to_string(GP) + "; i += 256) {");
         k.line("  const int ch = i / " + std::to_string(REP * PSZ) + ", rem = i % " + std::to_string(REP * PSZ) + ";");
-        k.line("  g_lds[i] = a.scratch[" + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + ") * " + std::to_string(PSZ) + " + rem];");
+        k.line("  g_lds[i] = sanic_ld(a.scratch + " + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + ") * " + std::to_string(PSZ) + " + rem);");
         k.line("}");
         k.line("__syncthreads();");
         src_expr = "g_lds[(ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + " + FIELD]";
     } else {
-        src_expr = "a.scratch[" + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + " + FIELD]";
+        src_expr = "sanic_ld(a.scratch + " + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + " + FIELD)";
     }
-    k.line("if (tid == 0) *cnt = 0u;");
+    k.line("if (tid == 0) sanic_st(cnt, 0u);");
     k.line("for (int pt = tid; pt < " + std::to_string(REP * E) + "; pt += 256) {");
     k.indent++;
     k.line("const int r = pt / " + std::to_string(E) + ", ee = pt % " + std::to_string(E) + ";");

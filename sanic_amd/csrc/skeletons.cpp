@@ -408,7 +408,7 @@ static std::string gemv_prologue(Renderer& R, const sanic_program_desc* d, const
     return pc.str();
 }
 
-static void gemv_finish(Renderer& R, Code& code, const sanic_program_desc* d, const GemvPlan& P) {
+static void gemv_finish(Renderer& R, Code& code, const sanic_program_desc* d, const GemvPlan& P, bool coherent) {
     const sanic_stage& st = d->stages[P.stage];
     const sanic_carrier& c = st.carrier;
     for (size_t i = 0; i < P.cslots.size(); i++)
@@ -426,7 +426,7 @@ static void gemv_finish(Renderer& R, Code& code, const sanic_program_desc* d, co
         v = R.value(code, st.epilogue, gc);
         R.memo.pop_back();
     }
-    code.line(store_stmt(R.param(st.out_buffer), "nn", st.out_dtype, v));
+    code.line(store_stmt(R.param(st.out_buffer), "nn", st.out_dtype, v, coherent));
 }
 
 // ───────────────────────── in-place row write (emit_metal.rs:1103-1178) ───────────────────
@@ -533,18 +533,17 @@ void emit_tail(Renderer& R, Code& k, const sanic_program_desc* d, const std::vec
     k.line("{");
     k.indent++;
     k.line("__shared__ int sanic_last;");
-    k.line("__threadfence();");
+    k.line("__builtin_amdgcn_s_waitcnt(0);");
     k.line("__syncthreads();");
-    k.line("if (threadIdx.x == 0) sanic_last = atomicAdd(" + counter + ", 1u) == (" + expected + ") - 1;");
+    k.line("if (threadIdx.x == 0) sanic_last = __hip_atomic_fetch_add(" + counter + ", 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (" + expected + ") - 1;");
     k.line("__syncthreads();");
     k.line("if (sanic_last) {");
     k.indent++;
-    k.line("__threadfence();");
     for (size_t i = 0; i < tails.size(); i++) {
-        if (i) k.line("__threadfence(); __syncthreads();");
+        if (i) k.line("__syncthreads();");
         emit_pointwise_loop(R, k, d, tails[i], "(idx_t)threadIdx.x", 256);
     }
-    k.line("if (threadIdx.x == 0) *" + counter + " = 0u;");
+    k.line("if (threadIdx.x == 0) sanic_st(" + counter + ", 0u);");
     k.indent--;
     k.line("}");
     k.indent--;
@@ -595,15 +594,19 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
 
     Renderer R(d);
     std::string prologue = gemv_prologue(R, d, P0);
+    for (auto& P : group) R.coherent.insert(d->stages[P.stage].out_buffer);
     const int64_t K = P0.K;
     const int SC = (int)P0.cslots.size(), SR = (int)P0.rslots.size();
     int64_t NTOT = 0;
     std::vector<int64_t> seg_off;
     for (auto& P : group) { seg_off.push_back(NTOT); NTOT += P.N; }
     const int KI = (int)((K + 511) / 512);
-    const int RQ = K <= 2048 ? 2 : 1;            // rows in flight per wave iteration
+    int RQ = K <= 2048 ? 2 : 1;                  // rows in flight per wave iteration
+    if (const char* e = getenv("SANIC_GEMV_RQ")) RQ = std::max(1, std::min(4, atoi(e)));
     int64_t waves = (NTOT + RQ - 1) / RQ;
-    int64_t blocks = std::min<int64_t>((waves + 3) / 4, 1024);
+    int64_t max_blocks = 1024;
+    if (const char* e = getenv("SANIC_GEMV_BLOCKS")) max_blocks = std::max(1, atoi(e));
+    int64_t blocks = std::min<int64_t>((waves + 3) / 4, max_blocks);
     int64_t counter_off = -1;
     if (!tails.empty()) {
         counter_off = scratch;
@@ -716,7 +719,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
                 c.line(std::string(g ? "} else " : "") + "if (seg" + qs + " == " + std::to_string(g) + ") {");
                 c.indent++;
                 R.memo.emplace_back();
-                gemv_finish(R, c, d, group[g]);
+                gemv_finish(R, c, d, group[g], !tails.empty());
                 R.memo.pop_back();
                 c.indent--;
             }
@@ -737,8 +740,13 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         c.s << lc.str();
         if (first) {
             // the row prologue runs while this iteration's weight loads are in flight
-            c.line("for (idx_t k = t; k < " + std::to_string(K) + "; k += 256) {");
+            // constant trip count, fully unrolled: every prologue load is issued up front
+            c.line("#pragma unroll");
+            c.line("for (int it = 0; it < " + std::to_string((K + 255) / 256) + "; ++it) {");
+            c.line("  const idx_t k = t + (idx_t)it * 256;");
+            if (K % 256) c.line("  if (k < " + std::to_string(K) + ") {");
             c.s << prologue;
+            if (K % 256) c.line("  }");
             c.line("}");
             if (SR > 0) {
                 c.line("float* red = u_lds + " + std::to_string(SC * K) + ";");
