@@ -27,7 +27,10 @@ struct Renderer {
     int tmp = 0;
     std::string fold_var = "fold_v";
     std::map<int, std::string> subst;
-    std::set<int> coherent;                      // buffers read with device-coherent loads            // node id -> precomputed value expression
+    std::set<int> coherent;                      // buffers read with device-coherent loads
+    Code scalars;                                // rank-0 input loads hoisted to kernel entry
+    std::map<int, std::string> scalar_vars;
+    std::string entry() const { return scalars.str(); }            // node id -> precomputed value expression
     explicit Renderer(const sanic_program_desc* dd) : d(dd) { memo.emplace_back(); }
 
     std::string param(int buffer);

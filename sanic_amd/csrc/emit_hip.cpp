@@ -417,6 +417,16 @@ std::string Renderer::value(Code& code, int node, const std::vector<std::string>
     case SANIC_NODE_COORDINATE: return "((float)(" + c[n.dim] + "))";
     case SANIC_NODE_FOLD: return fold_var;
     case SANIC_NODE_INPUT: {
+        if (n.rank == 0 && !coherent.count(n.buffer)) {
+            // a scalar input (a position, a step count) is loaded once at kernel entry
+            auto sv = scalar_vars.find(n.buffer);
+            if (sv != scalar_vars.end()) return sv->second;
+            std::string v = "sc" + std::to_string(n.buffer);
+            scalars.indent = 1;
+            scalars.line("const float " + v + " = " + load(node, c) + ";");
+            scalar_vars[n.buffer] = v;
+            return v;
+        }
         out = fresh("v");
         code.line("const float " + out + " = " + load(node, c) + ";");
         break;
@@ -799,6 +809,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     int waves = st.sched.lane_stream ? std::max(1, std::min(16, st.sched.waves)) : 0;
     int chunk = std::max(1, st.sched.chunk);
     Renderer R(d);
+    for (int t : tails) R.coherent.insert(d->stages[t].out_buffer);
     Code body;
     body.indent = 1;
     std::ostringstream src;
@@ -822,7 +833,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
         body.line("}");
         emit_finish(R, body, st, "gid");
         src << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(256) sanic_fold(Args a) {\n"
-            << body.str() << "}\n";
+            << R.entry() << body.str() << "}\n";
         Launch ln{"sanic_fold", "", dim3((unsigned)((gvol + 255) / 256)), dim3(256), 0, R.arg_list()};
         L.launches.push_back(ln);
         L.source = src.str();
@@ -898,7 +909,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     if (split == 1) {
         emit_finish(R, body, st, "gid");
         src << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(" << nth
-            << ") sanic_fold(Args a) {\n" << body.str() << "}\n";
+            << ") sanic_fold(Args a) {\n" << R.entry() << body.str() << "}\n";
         Launch ln{"sanic_fold", "", dim3((unsigned)gvol), dim3(nth), 0, R.arg_list()};
         L.launches.push_back(ln);
         L.source = src.str();
@@ -946,7 +957,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
         }
         body.line("if (t == 0) sanic_st(cnt, 0u);");
         src << R.args_struct({"float* __restrict__ scratch"});
-        src << "extern \"C\" __global__ void __launch_bounds__(" << nth << ") sanic_fold_split(Args a) {\n" << body.str() << "}\n";
+        src << "extern \"C\" __global__ void __launch_bounds__(" << nth << ") sanic_fold_split(Args a) {\n" << R.entry() << body.str() << "}\n";
         std::vector<Arg> args = R.arg_list();
         args.push_back({Arg::SCRATCH, part_off});
         L.launches.push_back({"sanic_fold_split", "", dim3((unsigned)(gvol * split)), dim3(nth), 0, args});
@@ -965,8 +976,8 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     // both kernels share one Args layout: the union of their buffers
     for (int b : R2.bufs) R.param(b);
     src << R.args_struct({"float* __restrict__ scratch"});
-    src << "extern \"C\" __global__ void __launch_bounds__(" << nth << ") sanic_fold_part(Args a) {\n" << body.str() << "}\n";
-    src << "extern \"C\" __global__ void __launch_bounds__(256) sanic_fold_merge(Args a) {\n" << mb.str() << "}\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(" << nth << ") sanic_fold_part(Args a) {\n" << R.entry() << body.str() << "}\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) sanic_fold_merge(Args a) {\n" << R2.entry() << mb.str() << "}\n";
     std::vector<Arg> args = R.arg_list();
     args.push_back({Arg::SCRATCH, part_off});
     L.launches.push_back({"sanic_fold_part", "", dim3((unsigned)(gvol * split)), dim3(nth), 0, args});
@@ -1003,7 +1014,7 @@ LoweredStage lower_pointwise(const sanic_program_desc* d, int si) {
     body.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v));
     std::ostringstream src;
     src << kPrelude << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(256) sanic_pointwise(Args a) {\n"
-        << body.str() << "}\n";
+        << R.entry() << body.str() << "}\n";
     L.source = src.str();
     L.launches.push_back({"sanic_pointwise", "", dim3((unsigned)((gvol + 255) / 256)), dim3(256), 0, R.arg_list()});
     return L;

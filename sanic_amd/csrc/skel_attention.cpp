@@ -282,8 +282,44 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("  }");
     k.line("} else {");
     k.line("const idx_t t1 = t0 + " + std::to_string(CH) + " < hi0 ? t0 + " + std::to_string(CH) + " : hi0;");
-    // query vectors (the A side, rendered) into LDS
-    k.line("for (int i = tid; i < " + std::to_string(REP * HD) + "; i += 256) {");
+    // ── prefetch: every K row and V run of this chunk is requested before any compute ──
+    const int LPT = 4;                                   // lanes per key position
+    const int64_t DPL = HD / LPT;                        // contiguous d per lane (multiple of 8)
+    const int NP = CH / 64;                              // score passes (64 positions each)
+    int repk; int64_t kt, kd, kh;
+    addr_parts(P.dot.kacc.addr, repk, NH, kt, kd, kh);
+    int repv; int64_t vt, ve, vh;
+    addr_parts(P.vacc.addr, repv, NH, vt, ve, vh);
+    const bool vfast = vt == 1 && E <= 64;
+    k.line("const unsigned short* __restrict__ kp = " + R.param(P.dot.kacc.buffer) + " + " + std::to_string(P.dot.kacc.addr.c0) +
+           " + grp * " + std::to_string(kh) + ";");
+    k.line("const unsigned short* __restrict__ vp = " + R.param(P.vacc.buffer) + " + " + std::to_string(P.vacc.addr.c0) +
+           " + grp * " + std::to_string(vh) + ";");
+    k.line("const int sub = tid % " + std::to_string(LPT) + ";");
+    k.line("sanic_u32x4 kq[" + std::to_string(NP) + "][" + std::to_string(DPL / 8) + "];");
+    k.line("#pragma unroll");
+    k.line("for (int ps = 0; ps < " + std::to_string(NP) + "; ++ps) {");
+    k.line("  const idx_t t = t0 + ps * 64 + tid / " + std::to_string(LPT) + ";");
+    k.line("  const idx_t tt = t < t1 ? t : t0;");
+    k.line("  #pragma unroll");
+    k.line("  for (int v8 = 0; v8 < " + std::to_string(DPL / 8) + "; ++v8)");
+    k.line("    kq[ps][v8] = *(const sanic_u32x4*)(kp + tt * " + std::to_string(kt) + " + sub * " + std::to_string(DPL) + " + v8 * 8);");
+    k.line("}");
+    k.line("const int e_ = tid % 64, tg = tid / 64;");   // value phase: lane = value dim, 4 groups of CH/4 positions
+    if (vfast) {
+        k.line("sanic_u32x4 vq[" + std::to_string(NP) + "][2];");
+        k.line("#pragma unroll");
+        k.line("for (int sb = 0; sb < " + std::to_string(NP) + "; ++sb) {");
+        k.line("  const idx_t tb = t0 + tg * " + std::to_string(CH / 4) + " + sb * 16;");
+        k.line("  const bool full = tb + 16 <= t1 && e_ < " + std::to_string(E) + ";");
+        k.line("  const unsigned short* src = vp + (full ? (idx_t)e_ * " + std::to_string(ve) + " + tb : 0);");
+        k.line("  vq[sb][0] = *(const sanic_u32x4*)(src);");
+        k.line("  vq[sb][1] = *(const sanic_u32x4*)(src + 8);");
+        k.line("}");
+    }
+    // query vectors (the A side, rendered) into LDS, after the K/V prefetch is issued: its latency hides behind the q-side arithmetic
+    if (REP * HD == 256) k.line("{ const int i = tid;");
+    else k.line("for (int i = tid; i < " + std::to_string(REP * HD) + "; i += 256) {");
     k.indent++;
     k.line("const idx_t hq = grp * " + std::to_string(REP) + " + i / " + std::to_string(HD) + ";");
     k.line("const idx_t dd = i % " + std::to_string(HD) + ";");
@@ -296,30 +332,20 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.indent--;
     k.line("}");
     k.line("__syncthreads();");
-    // scores: LPT lanes per position, each lane DPL = HD / LPT contiguous d
-    const int LPT = 4;
-    const int64_t DPL = HD / LPT;
-    const int64_t TPP = 256 / LPT;   // positions per pass
-    int repk; int64_t kt, kd, kh;
-    addr_parts(P.dot.kacc.addr, repk, NH, kt, kd, kh);
-    int64_t kbase = P.dot.kacc.addr.c0;
-    k.line("const unsigned short* __restrict__ kp = " + R.param(P.dot.kacc.buffer) + " + " + std::to_string(kbase) + " + grp * " + std::to_string(kh) + ";");
+    // scores
     k.line("#pragma unroll");
-    k.line("for (int pass = 0; pass < " + std::to_string((CH + TPP - 1) / TPP) + "; ++pass) {");
+    k.line("for (int ps = 0; ps < " + std::to_string(NP) + "; ++ps) {");
     k.indent++;
-    k.line("const int tl = pass * " + std::to_string(TPP) + " + tid / " + std::to_string(LPT) + ";");
-    k.line("const int sub = tid % " + std::to_string(LPT) + ";");
+    k.line("const int tl = ps * 64 + tid / " + std::to_string(LPT) + ";");
     k.line("const idx_t t = t0 + tl;");
     k.line("float dot[" + std::to_string(REP) + "];");
     k.line("#pragma unroll");
     k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) dot[r] = 0.0f;");
-    k.line("if (tl < " + std::to_string(CH) + " && t < t1) {");
-    k.indent++;
     k.line("#pragma unroll");
     k.line("for (int v8 = 0; v8 < " + std::to_string(DPL / 8) + "; ++v8) {");
     k.indent++;
     k.line("const int d0 = sub * " + std::to_string(DPL) + " + v8 * 8;");
-    k.line("const uint4 kv = *(const uint4*)(kp + t * " + std::to_string(kt) + " + d0);");
+    k.line("const sanic_u32x4 kv = kq[ps][v8];");
     k.line("const float kf[8] = {__uint_as_float(kv.x << 16), __uint_as_float(kv.x & 0xFFFF0000u), __uint_as_float(kv.y << 16), __uint_as_float(kv.y & 0xFFFF0000u), __uint_as_float(kv.z << 16), __uint_as_float(kv.z & 0xFFFF0000u), __uint_as_float(kv.w << 16), __uint_as_float(kv.w & 0xFFFF0000u)};");
     k.line("#pragma unroll");
     k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r)");
@@ -327,14 +353,12 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("  for (int j = 0; j < 8; ++j) dot[r] = fmaf(q_lds[r * " + std::to_string(HD) + " + d0 + j], kf[j], dot[r]);");
     k.indent--;
     k.line("}");
-    k.indent--;
-    k.line("}");
     k.line("#pragma unroll");
     k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) {");
     k.line("  #pragma unroll");
     k.line("  for (int off = 1; off < " + std::to_string(LPT) + "; off <<= 1) dot[r] += __shfl_xor(dot[r], off, 64);");
     k.line("}");
-    k.line("if (sub == 0 && tl < " + std::to_string(CH) + ") {");
+    k.line("if (sub == 0) {");
     k.indent++;
     k.line("const idx_t s = t;");
     for (int r = 0; r < REP; r++) {
@@ -347,8 +371,8 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         const sanic_node& sl = d->nodes[st.leaf[P.sleaf]];
         std::vector<std::string> lc(sl.rank);
         for (int j = 0; j < sl.rank; j++) {
-            int b = st.bind[P.sleaf][j];
-            lc[j] = b == SANIC_BIND_STREAM ? "s" : b == P.hdim ? "(grp * " + std::to_string(REP) + " + " + std::to_string(r) + ")" : "0";
+            int bd = st.bind[P.sleaf][j];
+            lc[j] = bd == SANIC_BIND_STREAM ? "s" : bd == P.hdim ? "(grp * " + std::to_string(REP) + " + " + std::to_string(r) + ")" : "0";
         }
         std::string v = R.value(k, st.leaf[P.sleaf], lc);
         R.subst.clear();
@@ -380,24 +404,18 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("}");
     k.line("__syncthreads();");
     // o[r][e] = Σ_t p[r][t] · V(h, t, e)
-    int repv; int64_t vt, ve, vh;
-    addr_parts(P.vacc.addr, repv, NH, vt, ve, vh);
-    int64_t vbase = P.vacc.addr.c0;
-    k.line("const unsigned short* __restrict__ vp = " + R.param(P.vacc.buffer) + " + " + std::to_string(vbase) + " + grp * " + std::to_string(vh) + ";");
-    k.line("for (int e = tid % 64; e < " + std::to_string(E) + "; e += 64) {");
+    k.line("for (int e = e_; e < " + std::to_string(E) + "; e += 64) {");
     k.indent++;
-    k.line("const int tg = tid / 64;");   // 4 groups of CH/4 positions, in runs of 16
     k.line("float o[" + std::to_string(REP) + "];");
     k.line("#pragma unroll");
     k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = 0.0f;");
     k.line("#pragma unroll");
-    k.line("for (int sb = 0; sb < " + std::to_string(CH / 64) + "; ++sb) {");
+    k.line("for (int sb = 0; sb < " + std::to_string(NP) + "; ++sb) {");
+    k.indent++;
     k.line("const int tbase = tg * " + std::to_string(CH / 4) + " + sb * 16;");
-    if (vt == 1) {
+    if (vfast) {
         k.line("if (t0 + tbase + 16 <= t1) {");
-        k.line("  const uint4 va = *(const uint4*)(vp + e * " + std::to_string(ve) + " + t0 + tbase);");
-        k.line("  const uint4 vb = *(const uint4*)(vp + e * " + std::to_string(ve) + " + t0 + tbase + 8);");
-        k.line("  const unsigned vw[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};");
+        k.line("  const unsigned vw[8] = {vq[sb][0].x, vq[sb][0].y, vq[sb][0].z, vq[sb][0].w, vq[sb][1].x, vq[sb][1].y, vq[sb][1].z, vq[sb][1].w};");
         k.line("  #pragma unroll");
         k.line("  for (int j = 0; j < 16; ++j) {");
         k.line("    const float vf = __uint_as_float((j & 1) ? (vw[j >> 1] & 0xFFFF0000u) : (vw[j >> 1] << 16));");
@@ -422,6 +440,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("  }");
         k.line("}");
     }
+    k.indent--;
     k.line("}");
     k.line("#pragma unroll");
     k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) o_lds[tg][r][e] = o[r];");
@@ -529,7 +548,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const std::string kpart = "sanic_attn_decode_" + tag;
     std::ostringstream src;
     src << kPrelude << R.args_struct({"float* __restrict__ scratch"});
-    src << "extern \"C\" __global__ void __launch_bounds__(256) " << kpart << "(Args a) {\n" << k.str() << "}\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << kpart << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     out.kernel_kind = "skeleton:attn_decode[rep " + std::to_string(REP) + "]";
     out.source = src.str();
     std::vector<Arg> args = R.arg_list();

@@ -530,6 +530,8 @@ bool tail_candidate(const sanic_program_desc* d, int si) {
 void emit_tail(Renderer& R, Code& k, const sanic_program_desc* d, const std::vector<int>& tails, const std::string& counter,
                const std::string& expected) {
     if (tails.empty()) return;
+    // data the tails write is never hoisted or cached across them
+    for (int t : tails) R.coherent.insert(d->stages[t].out_buffer);
     k.line("{");
     k.indent++;
     k.line("__shared__ int sanic_last;");
@@ -781,7 +783,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
     const std::string kname = "sanic_gemv_" + std::to_string(NTOT) + "x" + std::to_string(K);
     std::ostringstream src;
     src << kPrelude << R.args_struct(tails.empty() ? std::vector<std::string>{} : std::vector<std::string>{"float* __restrict__ scratch"})
-        << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << k.str() << "}\n";
+        << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     LoweredStage L;
     L.kernel_kind = "skeleton:gemv" + std::string(group.size() > 1 ? "[batched " + std::to_string(group.size()) + "]" : "") +
                     (tails.empty() ? "" : "+tail" + std::to_string(tails.size()));
@@ -814,7 +816,7 @@ bool lower_pointwise_skeleton(const sanic_program_desc* d, int si, int64_t&, Low
     emit_pointwise_loop(R, body, d, si, "((idx_t)blockIdx.x * 256 + threadIdx.x)", (int)std::min<int64_t>(work, 1 << 30));
     std::ostringstream src;
     src << kPrelude << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(256) sanic_rowwrite(Args a) {\n"
-        << body.str() << "}\n";
+        << R.entry() << body.str() << "}\n";
     out.kernel_kind = "skeleton:rowwrite";
     out.source = src.str();
     out.launches.push_back({"sanic_rowwrite", "", dim3((unsigned)((work + 255) / 256)), dim3(256), 0, R.arg_list()});

@@ -307,12 +307,16 @@ def rope(x: Node, position: Node, inv_freq: Node) -> Node:
     """Rotate-half RoPE over the trailing head dim (nn.rs:171-194): split the head dim into
     (pair=2, frequency=F); out = x·cos(angle) + flip(x, pair)·sign·sin(angle), sign(pair) =
     2·pair − 1, angle[s, f] = (position + s·0)·inv_freq[f] broadcast over the sequence dim
-    x.shape[-2]."""
+    x.shape[-2]. A rank-1 `position` gives each row its own position (prefill)."""
     hd = x.shape[-1]
     F = hd // 2
     xs = split(x, -1, 2, F)                     # [..., seq, 2, F]
     seq = x.shape[-2]
-    pos = map_(ADD, map_(MUL, iota(seq), const(0.0)), position)   # [seq]
+    if position.rank == 0:
+        # the reference's form: every row of the sequence at `position` (decode)
+        pos = map_(ADD, map_(MUL, iota(seq), const(0.0)), position)   # [seq]
+    else:
+        pos = position                           # per-row positions [seq] (prefill)
     angle = map_(MUL, unsqueeze(pos, 1), unsqueeze(inv_freq, 0))   # [seq, F]
     angle = unsqueeze(angle, 1)                                    # [seq, 1, F]
     sign = unsqueeze(map_(SUB, map_(MUL, iota(2), const(2.0)), const(1.0)), 1)  # [2, 1]

@@ -1,0 +1,88 @@
+"""The C-ABI library without a GPU: it loads, exports every declared symbol, its records match
+the Python layouts, and it lowers and compiles every shipped configuration (hipRTC needs no GPU).
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from sanic_amd import abi, carrier as C, configs, ir
+from sanic_amd.program import STREAM, Program, Sched
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "sanic_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sanic_hip_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(abi.LIB_PATH)
+    names = declared_functions()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(abi.SIGNATURES), set(names) ^ set(abi.SIGNATURES)
+
+
+def test_record_layouts_match():
+    want, got = abi.check_layouts()
+    assert want == got
+
+
+def test_open_without_gpu_reports_backend_error():
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU is present")
+    h = ctypes.c_void_p()
+    st = abi.lib().sanic_hip_open(0, ctypes.byref(h))
+    assert st == 6 and not h.value   # SANIC_ERR_BACKEND (MetalDevice::open → None)
+
+
+@pytest.mark.parametrize("name", ["A", "A_coop", "A_split", "B1", "B1_rows", "D1", "C3", "E_stage"])
+def test_lowering_chooses_the_expected_kernel(name):
+    progs = {
+        "A": (configs.direct_attention(), 0, "fold:scalar"),
+        "A_coop": (configs.direct_attention(sched=Sched(lane_stream=True, waves=2)), 0, "fold:coop"),
+        "A_split": (configs.direct_attention(sched=Sched(lane_stream=True, waves=2, split=4)), 0, "fold:split"),
+        "B1": (configs.rmsnorm_projection(kmajor=True), 0, ""),
+        "B1_rows": (configs.rmsnorm_projection(kmajor=False), 0, "skeleton:gemv"),
+        "D1": (configs.int4_matmul(), 0, "skeleton:gemv"),
+        "C3": (configs.decode_attention(), 0, "skeleton:attn_decode"),
+        "E_stage": (configs.llama_decode(), 1, "skeleton:gemv[batched 3]+tail2"),
+    }
+    p, stage, want = progs[name]
+    kind, src = p.emit(stage)
+    assert kind.startswith(want), kind
+    assert "extern \"C\" __global__" in src
+
+
+def test_precompile_small_program():
+    configs.direct_attention(S=16, D=8).precompile()
+
+
+def test_validation_rejects_bad_programs():
+    p = Program()
+    x = p.input("X", (4, 4))
+    p.fused("Y", (4,), 4, [(x, (0, STREAM))], C.plain(ir.M_ADD))
+    p.stages[0].grid = (5,)                 # grid no longer matches the output buffer
+    with pytest.raises(abi.SanicError) as e:
+        p.emit(0)
+    assert e.value.code == 1
+    q = Program()
+    y = q.input("X", (4, 4))
+    q.fused("Y", (4,), 4, [(y, (0, 1))], C.plain(ir.M_ADD))   # binding refers to a grid dim of extent 4? no: dim 1 absent
+    with pytest.raises(abi.SanicError):
+        q.emit(0)
+
+
+def test_unpadded_out_of_bounds_reindex_is_rejected():
+    p = Program()
+    x = p.input("X", (4,))
+    shifted = ir.reindex(x, (4,), [(((1, 0),), 1)], padded=False)   # reads X[i + 1]
+    p.pointwise("Y", shifted, ir.F32)
+    with pytest.raises(abi.SanicError):
+        p.emit(0)
