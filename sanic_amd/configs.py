@@ -30,12 +30,42 @@ def direct_attention(S: int = 128, D: int = 64, causal: bool = True, dtype: int 
     return p
 
 
+def flash_prefill(NH: int = 32, NKV: int = 8, S: int = 4096, HD: int = 64, theta: float = 500000.0,
+                  window: int = 0, rope_stages: bool = True) -> Program:
+    """Config C (prefill): GQA causal attention over S tokens, RoPE (rotate-half, plain
+    inv_freq, each row at its own position) on Q and K, scale 1/√HD; `window` > 0 adds the
+    sliding-window mask (key visible iff q − window + 1 ≤ k ≤ q). The RoPE'd Q and K are
+    materialised by two pointwise stages (bf16), then one FlashAttention carrier fold."""
+    p = Program()
+    q = p.input("Q", (NH, S, HD), ir.BF16)
+    k = p.input("K", (NKV, S, HD), ir.BF16)
+    v = p.input("V", (NKV, S, HD), ir.BF16)
+    if rope_stages:
+        invf = ir.rope_inv_freq(theta, HD // 2)
+        rows = ir.iota(S)
+        q = p.pointwise("Qr", ir.rope(q, rows, invf), ir.BF16, role=3)
+        k = p.pointwise("Kr", ir.rope(k, rows, invf), ir.BF16, role=3)
+    rep = NH // NKV
+    scores = ir.reduce(ir.map_(ir.MUL, ir.unsqueeze(q, 2), ir.unsqueeze(ir.expand_heads(k, 0, rep), 1)), 3, ir.M_ADD)
+    scores = ir.map_(ir.MUL, scores, ir.const(1.0 / math.sqrt(HD)))            # [NH, S, S]
+    scores = ir.map_(ir.ADD, scores, ir.causal_mask_like(scores, 1, 2))
+    if window:
+        # key visible iff k ≥ q − window + 1:  mask where(k < q − (window − 1), −1e30, 0)
+        lo = ir.map_(ir.SUB, ir.coordinate(scores, 1), ir.const(float(window - 1)))
+        scores = ir.map_(ir.ADD, scores, ir.map_(ir.WHERE, ir.map_(ir.LT, ir.coordinate(scores, 2), lo),
+                                                  ir.const(-1e30), ir.const(0.0)))
+    vexp = ir.expand_heads(v, 0, rep)                                            # [NH, S, HD]
+    p.fused("O", (NH, S, HD), S, [(scores, (0, 1, STREAM)), (vexp, (0, STREAM, 2))],
+            C.online_softmax_weighted(), ir.BF16)
+    return p
+
+
 def precompile_all() -> None:
     """Fill the code-object cache with every shipped configuration's kernels."""
     for s in (None, Sched(lane_stream=True, waves=1), Sched(lane_stream=True, waves=2, split=4)):
         direct_attention(sched=s).precompile()
     for p in (rmsnorm_projection(kmajor=False), rmsnorm_projection(kmajor=True), int4_matmul(),
-              decode_attention(), llama_decode()):
+              decode_attention(), llama_decode(), flash_prefill(), flash_prefill(window=1024)):
         p.precompile()
 
 

@@ -47,6 +47,7 @@ struct WindowBound {
     enum Kind { HI_FLOOR_PLUS1, HI_CEIL, LO_CEIL } kind;
     int node;                 // the stream-independent edge expression
     std::vector<int> bind;    // its dims' bindings
+    int where_node = -1;      // the additive mask term this bound was read from
 };
 
 extern const char* kPrelude;

@@ -686,9 +686,9 @@ static void collect_window(const sanic_program_desc* d, int node, const std::vec
     bool l_dep = depends_on_stream(d, cond.in[0], lb), r_dep = depends_on_stream(d, cond.in[1], rb);
     bool t_big = is_big_negative(d, n.in[1]), t_zero = is_zero(d, n.in[1]);
     bool f_big = is_big_negative(d, n.in[2]), f_zero = is_zero(d, n.in[2]);
-    if (r_s && !l_dep && t_big && f_zero) out.push_back({WindowBound::HI_FLOOR_PLUS1, cond.in[0], lb});
-    else if (l_s && !r_dep && t_zero && f_big) out.push_back({WindowBound::HI_CEIL, cond.in[1], rb});
-    else if (l_s && !r_dep && t_big && f_zero) out.push_back({WindowBound::LO_CEIL, cond.in[1], rb});
+    if (r_s && !l_dep && t_big && f_zero) out.push_back({WindowBound::HI_FLOOR_PLUS1, cond.in[0], lb, node});
+    else if (l_s && !r_dep && t_zero && f_big) out.push_back({WindowBound::HI_CEIL, cond.in[1], rb, node});
+    else if (l_s && !r_dep && t_big && f_zero) out.push_back({WindowBound::LO_CEIL, cond.in[1], rb, node});
 }
 
 // Window bounds for a fused stage: only when the carrier has an ExpShifted slot whose max slot's

@@ -1,0 +1,522 @@
+// FlashAttention prefill skeleton: the online-softmax (m, ℓ, o) carrier over the key axis on
+// bf16 MFMA (v_mfma_f32_16x16x32_bf16), for stages whose query grid has a head axis and a
+// query-row axis (the causal / sliding-window prefill of the reference's
+// scaled_dot_product_attention, /root/reference/src/nn.rs:27-105, folded as
+// /root/reference/tests/laws.rs:108-126).
+//
+// Structure required (read from the carrier and the leaves, never from names): the carrier of
+// skel_attention.cpp (a Plain(Max) score slot, ExpShifted slots with constant or value `into`);
+// the score leaf = one in-body contraction Σ_d Q·K (both affine bf16 views with d contiguous,
+// the head entering K as ⌊h/rep⌋) with scalar factors and additive mask terms around it; the
+// value leaf an affine bf16 view.
+//
+// Kernel shape (one workgroup = one head × 128 query rows, 4 waves × 32 rows):
+//   S^T = K·Q^T per 64-key tile (so a lane owns one query column: the running max, the sum and
+//   the O rescale are lane-local, with one 4-lane shuffle per tile for the max);
+//   O^T += V^T·P^T with P packed to bf16 in registers (the MFMA k-order is chosen to match the
+//   S^T accumulator layout, so P never goes through LDS);
+//   K and V^T tiles are double-buffered in LDS; exp2 with log2(e) folded; the −∞ guard of the
+//   carrier's combine on the rescale; tiles outside every row's honest window are skipped and
+//   tiles entirely inside it skip the mask arithmetic;
+//   blockIdx → (KV head, query head, query block) places all query heads of one KV head on one
+//   XCD (blockIdx mod 8) so their K/V stay in that XCD's L2, heaviest causal blocks first.
+#include <algorithm>
+#include <cmath>
+
+#include "emit.h"
+#include "skeletons.h"
+
+namespace sanic {
+
+namespace {
+
+struct FlashPlan {
+    int sleaf = -1, vleaf = -1, max_slot = -1;
+    std::vector<int> vec_slots, scalar_slots;
+    std::vector<double> scalar_into;
+    int hdim = -1, qdim = -1, edim = -1;
+    int64_t NH = 1, NQ = 1, E = 1, T = 1, HD = 1;
+    int rep = 1;
+    int dot_reduce = -1;
+    Access qacc, kacc, vacc;
+};
+
+bool sym_is_var(const Sym& s, int& var) {
+    if (s.c0 != 0 || s.terms.size() != 1) return false;
+    const SymTerm& t = s.terms[0];
+    if (t.coef != 1 || t.div != 1 || t.mod != 0) return false;
+    var = t.var;
+    return true;
+}
+
+// address = c0 + Σ terms; returns per-var coefficient (div 1, no mod) and the h term's div
+bool split_addr(const Sym& a, int nvars, std::vector<int64_t>& coef, int& hdiv, int64_t& hcoef) {
+    coef.assign(nvars, 0);
+    hdiv = 0;
+    hcoef = 0;
+    for (auto& t : a.terms) {
+        if (t.mod) return false;
+        if (t.var == 0 && t.div != 1) {
+            if (hdiv) return false;
+            hdiv = (int)t.div;
+            hcoef = t.coef;
+            continue;
+        }
+        if (t.div != 1) return false;
+        coef[t.var] += t.coef;
+    }
+    return true;
+}
+
+bool find_flash_dot(const sanic_program_desc* d, int node, const std::vector<Sym>& c, const std::vector<int64_t>& ext,
+                    FlashPlan& P) {
+    const sanic_node& n = d->nodes[node];
+    if (n.kind == SANIC_NODE_MAP) {
+        int found = 0;
+        for (int k = 0; k < n.n_in; k++) {
+            const sanic_node& m = d->nodes[n.in[k]];
+            bool has_reduce = false;
+            std::vector<int> st{n.in[k]};
+            while (!st.empty()) {
+                int i = st.back(); st.pop_back();
+                if (d->nodes[i].kind == SANIC_NODE_REDUCE) has_reduce = true;
+                for (int q = 0; q < d->nodes[i].n_in; q++) st.push_back(d->nodes[i].in[q]);
+            }
+            if (!has_reduce) continue;
+            int lead = n.rank - m.rank;
+            std::vector<Sym> cc(m.rank);
+            for (int j = 0; j < m.rank; j++) cc[j] = m.shape[j] == 1 ? Sym() : c[lead + j];
+            if (!find_flash_dot(d, n.in[k], cc, ext, P)) return false;
+            found++;
+        }
+        return found == 1;
+    }
+    if (n.kind != SANIC_NODE_REDUCE || n.op != SANIC_MON_ADD) return false;
+    const sanic_node& mp = d->nodes[n.in[0]];
+    if (mp.kind != SANIC_NODE_MAP || mp.op != SANIC_OP_MUL) return false;
+    // vars: 0 = head, 1 = key (stream), 2 = contraction d, 3 = query row
+    std::vector<Sym> mc;
+    for (int j = 0, o = 0; j < mp.rank; j++) mc.push_back(j == n.dim ? Sym::var(2) : c[o++]);
+    std::vector<int64_t> ext4 = {ext[0], ext[1], mp.shape[n.dim], ext[3]};
+    int kside = -1;
+    std::vector<std::vector<Sym>> cc(2);
+    for (int k = 0; k < 2; k++) {
+        const sanic_node& ch = d->nodes[mp.in[k]];
+        int lead = mp.rank - ch.rank;
+        cc[k].resize(ch.rank);
+        bool moves = false;
+        for (int j = 0; j < ch.rank; j++) {
+            cc[k][j] = ch.shape[j] == 1 ? Sym() : mc[lead + j];
+            for (auto& t : cc[k][j].terms) moves |= t.var == 1;
+        }
+        if (moves) {
+            if (kside >= 0) return false;
+            kside = k;
+        }
+    }
+    if (kside < 0) return false;
+    if (!sym_access(d, mp.in[kside], cc[kside], ext4, P.kacc)) return false;
+    if (!sym_access(d, mp.in[1 - kside], cc[1 - kside], ext4, P.qacc)) return false;
+    P.dot_reduce = node;
+    P.HD = mp.shape[n.dim];
+    return true;
+}
+
+bool flash_plan(const sanic_program_desc* d, int si, FlashPlan& P) {
+    const sanic_stage& st = d->stages[si];
+    if (st.kind != SANIC_STAGE_FUSED || st.n_leaves != 2) return false;
+    const sanic_carrier& c = st.carrier;
+    P = FlashPlan();
+    for (int k = 0; k < c.slots; k++)
+        if (c.kind[k].kind == SANIC_SLOT_PLAIN && c.kind[k].monoid == SANIC_MON_MAX) {
+            if (P.max_slot >= 0) return false;
+            P.max_slot = k;
+        }
+    if (P.max_slot < 0) return false;
+    const sanic_expr& mi = d->exprs[c.into[P.max_slot]];
+    if (mi.op != SANIC_EX_ITEM) return false;
+    P.sleaf = mi.index;
+    for (int k = 0; k < c.slots; k++) {
+        if (k == P.max_slot) continue;
+        if (c.kind[k].kind != SANIC_SLOT_EXP_SHIFTED || c.kind[k].ref_slot != P.max_slot) return false;
+        const sanic_expr& e = d->exprs[c.into[k]];
+        if (e.op == SANIC_EX_ITEM && e.index != P.sleaf) {
+            if (P.vleaf >= 0 && P.vleaf != e.index) return false;
+            P.vleaf = e.index;
+            P.vec_slots.push_back(k);
+        } else if (e.op == SANIC_EX_CONST) {
+            P.scalar_slots.push_back(k);
+            P.scalar_into.push_back(e.value);
+        } else {
+            return false;
+        }
+    }
+    if (P.vleaf < 0 || P.vec_slots.size() != 1) return false;
+    const sanic_node& sl = d->nodes[st.leaf[P.sleaf]];
+    const sanic_node& vl = d->nodes[st.leaf[P.vleaf]];
+    std::vector<bool> in_s(st.rank, false), in_v(st.rank, false);
+    for (int j = 0; j < sl.rank; j++) if (st.bind[P.sleaf][j] >= 0) in_s[st.bind[P.sleaf][j]] = true;
+    for (int j = 0; j < vl.rank; j++) if (st.bind[P.vleaf][j] >= 0) in_v[st.bind[P.vleaf][j]] = true;
+    std::vector<int> qdims;
+    for (int j = 0; j < st.rank; j++) {
+        if (st.grid[j] == 1) continue;
+        if (in_v[j] && !in_s[j]) {
+            if (P.edim >= 0) return false;
+            P.edim = j;
+        } else {
+            qdims.push_back(j);
+        }
+    }
+    if (P.edim < 0 || qdims.size() != 2) return false;
+    // the head dim is the one the value leaf reads; the query row is read only by the score
+    for (int j : qdims) {
+        if (in_v[j]) P.hdim = j;
+        else P.qdim = j;
+    }
+    if (P.hdim < 0 || P.qdim < 0) return false;
+    P.NH = st.grid[P.hdim];
+    P.NQ = st.grid[P.qdim];
+    P.E = st.grid[P.edim];
+    P.T = st.stream;
+    std::vector<Sym> scs(sl.rank);
+    for (int j = 0; j < sl.rank; j++) {
+        int b = st.bind[P.sleaf][j];
+        scs[j] = b == SANIC_BIND_STREAM ? Sym::var(1) : b == P.hdim ? Sym::var(0) : b == P.qdim ? Sym::var(3) : Sym();
+    }
+    if (!find_flash_dot(d, st.leaf[P.sleaf], scs, {P.NH, P.T, 1, P.NQ}, P)) return false;
+    std::vector<Sym> vcs(vl.rank);
+    for (int j = 0; j < vl.rank; j++) {
+        int b = st.bind[P.vleaf][j];
+        vcs[j] = b == SANIC_BIND_STREAM ? Sym::var(1) : b == P.hdim ? Sym::var(0) : b == P.edim ? Sym::var(2) : Sym();
+    }
+    if (!sym_access(d, st.leaf[P.vleaf], vcs, {P.NH, P.T, P.E}, P.vacc)) return false;
+    if (P.qacc.dtype != SANIC_BF16 || P.kacc.dtype != SANIC_BF16 || P.vacc.dtype != SANIC_BF16) return false;
+    if (P.HD != 64 || P.E != 64 || P.NQ % 128 != 0 || P.T % 64 != 0) return false;
+    // Q: (h, d, i) with d contiguous; K: (⌊h/rep⌋, t, d) with d contiguous; V: (⌊h/rep⌋, t, e)
+    std::vector<int64_t> qc, kc, vc;
+    int qh, kh, vh;
+    int64_t qhc, khc, vhc;
+    if (!split_addr(P.qacc.addr, 4, qc, qh, qhc) || qh != 0) return false;
+    if (!split_addr(P.kacc.addr, 4, kc, kh, khc)) return false;
+    if (!split_addr(P.vacc.addr, 3, vc, vh, vhc)) return false;
+    if (qc[2] != 1 || qc[1] != 0 || kc[2] != 1 || kc[3] != 0 || (vc[2] != 1 && vc[1] != 1)) return false;
+    int repk = kh ? kh : (kc[0] ? 1 : (int)P.NH);
+    int repv = vh ? vh : (vc[0] ? 1 : (int)P.NH);
+    if (repk != repv) return false;
+    P.rep = repk;
+    return true;
+}
+
+}  // namespace
+
+bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
+    (void)scratch;
+    FlashPlan P;
+    if (!flash_plan(d, si, P)) return false;
+    const sanic_stage& st = d->stages[si];
+    const sanic_carrier& c = st.carrier;
+    const int64_t NH = P.NH, NQ = P.NQ, T = P.T, E = P.E, HD = P.HD;
+    const int64_t NQB = NQ / 128;
+    std::vector<int64_t> qc, kc, vc;
+    int qh, kh, vh;
+    int64_t qhc, khc, vhc;
+    split_addr(P.qacc.addr, 4, qc, qh, qhc);
+    split_addr(P.kacc.addr, 4, kc, kh, khc);
+    split_addr(P.vacc.addr, 3, vc, vh, vhc);
+    const bool v_rows = vc[2] == 1;                  // V[t, e] rows (else V^T with t contiguous)
+    auto hterm = [&](const std::vector<int64_t>& cf, int div, int64_t hcf) {
+        // address contribution of head hh
+        if (div) return "(hh / " + std::to_string(div) + ") * " + std::to_string(hcf);
+        return "hh * " + std::to_string(cf[0]);
+    };
+
+    Renderer R(d);
+    // score functions: the leaf with its contraction replaced by `dotv`; the "full" variant also
+    // drops the additive mask terms (used only on tiles every row sees entirely)
+    auto win = honest_window(d, st);
+    const sanic_node& sl = d->nodes[st.leaf[P.sleaf]];
+    std::vector<std::string> lc(sl.rank);
+    for (int j = 0; j < sl.rank; j++) {
+        int b = st.bind[P.sleaf][j];
+        lc[j] = b == SANIC_BIND_STREAM ? "kj" : b == P.hdim ? "hh" : b == P.qdim ? "qi" : "0";
+    }
+    Renderer Rs(d);
+    Code sp, sf;
+    sp.indent = sf.indent = 1;
+    Rs.subst[P.dot_reduce] = "dotv";
+    std::string vpart = Rs.value(sp, st.leaf[P.sleaf], lc);
+    std::string entry_part = Rs.entry();
+    Renderer Rf(d);
+    Rf.subst[P.dot_reduce] = "dotv";
+    for (auto& w : win) Rf.subst[w.where_node] = "0.0f";
+    std::string vfull = Rf.value(sf, st.leaf[P.sleaf], lc);
+    std::string entry_full = Rf.entry();
+    for (int b : Rs.bufs) R.param(b);
+    for (int b : Rf.bufs) R.param(b);
+
+    // window edges per query row (for tile skipping / full-tile detection)
+    Code wc;
+    wc.indent = 1;
+    Renderer Rw(d);
+    std::vector<std::string> gcw(st.rank, "0");
+    gcw[P.hdim] = "hh";
+    gcw[P.qdim] = "qrow";
+    {
+        Code tmp;
+        tmp.indent = 1;
+        // emit_window names grid coords g<j>
+        for (int j = 0; j < st.rank; j++) tmp.line("const idx_t g" + std::to_string(j) + " = " + gcw[j] + ";");
+        emit_window(Rw, tmp, st, win, "wlo", "whi");
+        wc.s << tmp.str();
+    }
+    for (int b : Rw.bufs) R.param(b);
+
+    // finish: project (+ epilogue) and the narrowing store of one output point
+    Renderer Ro(d);
+    Code fo;
+    fo.indent = 1;
+    {
+        for (int sl2 = 0; sl2 < c.slots; sl2++) fo.line("const float fs" + std::to_string(sl2) + " = fs[" + std::to_string(sl2) + "];");
+        std::string f = Ro.expr(fo, c.project, "", "", "", "fs");
+        fo.line("const float fold_v = " + f + ";");
+        std::vector<std::string> gc(st.rank, "0");
+        gc[P.hdim] = "hh";
+        gc[P.qdim] = "qi";
+        gc[P.edim] = "ee";
+        std::string v = "fold_v";
+        if (st.epilogue >= 0) {
+            Ro.fold_var = "fold_v";
+            v = Ro.value(fo, st.epilogue, gc);
+        }
+        std::string lin;
+        for (int j = 0; j < st.rank; j++)
+            lin = j == 0 ? "(idx_t)(" + gc[0] + ")" : "(" + lin + " * " + std::to_string(st.grid[j]) + " + (idx_t)(" + gc[j] + "))";
+        fo.line(store_stmt(Ro.param(st.out_buffer), lin, st.out_dtype, v));
+    }
+    for (int b : Ro.bufs) R.param(b);
+    std::string qp = R.param(P.qacc.buffer), kp = R.param(P.kacc.buffer), vp = R.param(P.vacc.buffer);
+
+    std::ostringstream src;
+    src << kPrelude;
+    src << "typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;\n";
+    src << "typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;\n";
+    src << R.args_struct({});
+    src << "__device__ __forceinline__ float score_part(const Args& a, float dotv, idx_t hh, idx_t qi, idx_t kj) {\n"
+        << entry_part << sp.str() << "  return " << vpart << ";\n}\n";
+    src << "__device__ __forceinline__ float score_full(const Args& a, float dotv, idx_t hh, idx_t qi, idx_t kj) {\n"
+        << entry_full << sf.str() << "  return " << vfull << ";\n}\n";
+    src << "__device__ __forceinline__ void window(const Args& a, idx_t hh, idx_t qrow, idx_t& lo, idx_t& hi) {\n"
+        << Rw.entry() << wc.str() << "  lo = wlo; hi = whi;\n}\n";
+    src << "__device__ __forceinline__ void finish(const Args& a, const float* fs, idx_t hh, idx_t qi, idx_t ee) {\n"
+        << Ro.entry() << fo.str() << "}\n";
+
+    const std::string kname = "sanic_flash_h" + std::to_string(NH) + "_s" + std::to_string(NQ) + "_t" + std::to_string(T);
+    Code k;
+    k.indent = 1;
+    const int KS = 72;      // LDS row stride (bf16) of the K tile: 64 + 8 padding
+    const int VS = 72;      // LDS row stride of the V^T tile
+    k.line("__shared__ unsigned short k_lds[2][64 * " + std::to_string(KS) + "];");
+    k.line("__shared__ unsigned short v_lds[2][64 * " + std::to_string(VS) + "];");
+    k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
+    k.line("const int l16 = lane & 15, lq = lane >> 4;");
+    // XCD-aware block order: blockIdx mod 8 picks the KV head group, heaviest query blocks first
+    const int64_t NKV = NH / P.rep;
+    k.line("const idx_t bid = blockIdx.x;");
+    if (NKV % 8 == 0 || NKV == 8) {
+        k.line("const idx_t kvh = bid % " + std::to_string(NKV) + ", rest = bid / " + std::to_string(NKV) + ";");
+        k.line("const idx_t hh = kvh * " + std::to_string(P.rep) + " + rest % " + std::to_string(P.rep) + ";");
+        k.line("const idx_t qb = " + std::to_string(NQB - 1) + " - rest / " + std::to_string(P.rep) + ";");
+    } else {
+        k.line("const idx_t hh = bid % " + std::to_string(NH) + ";");
+        k.line("const idx_t qb = " + std::to_string(NQB - 1) + " - bid / " + std::to_string(NH) + ";");
+    }
+    k.line("const idx_t q0 = qb * 128 + wv * 32;");   // this wave's 32 query rows
+    // block and wave key ranges from the honest window of the first and last rows
+    k.line("idx_t blo_a, bhi_a, blo_b, bhi_b, wlo_a, whi_a, wlo_b, whi_b;");
+    k.line("window(a, hh, qb * 128, blo_a, bhi_a);");
+    k.line("window(a, hh, qb * 128 + 127, blo_b, bhi_b);");
+    k.line("window(a, hh, q0, wlo_a, whi_a);");
+    k.line("window(a, hh, q0 + 31, wlo_b, whi_b);");
+    k.line("const idx_t klo = (blo_a < blo_b ? blo_a : blo_b) / 64 * 64;");
+    k.line("const idx_t khi = bhi_a > bhi_b ? bhi_a : bhi_b;");
+    k.line("const idx_t wlo = wlo_a < wlo_b ? wlo_a : wlo_b, whi = whi_a > whi_b ? whi_a : whi_b;");
+    k.line("const idx_t flo = wlo_a > wlo_b ? wlo_a : wlo_b, fhi = whi_a < whi_b ? whi_a : whi_b;");
+    // Q^T as the B operand: lane = query column l16 (+16·qt), d-slots lq·8 + 0..7 (+32·ds)
+    k.line("bf16x8 qf[2][2];");
+    k.line("#pragma unroll");
+    k.line("for (int qt = 0; qt < 2; ++qt)");
+    k.line("  #pragma unroll");
+    k.line("  for (int ds = 0; ds < 2; ++ds)");
+    k.line("    qf[qt][ds] = *(const bf16x8*)(" + qp + " + " + std::to_string(P.qacc.addr.c0) + " + " + hterm(qc, qh, qhc) +
+           " + (q0 + qt * 16 + l16) * " + std::to_string(qc[3]) + " + ds * 32 + lq * 8);");
+    k.line("f32x4 o[4][2];");
+    k.line("#pragma unroll");
+    k.line("for (int dt = 0; dt < 4; ++dt) { o[dt][0] = (f32x4){0, 0, 0, 0}; o[dt][1] = (f32x4){0, 0, 0, 0}; }");
+    k.line("float m_run[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};");
+    k.line("float l_run[2] = {0.0f, 0.0f};");
+    const double LOG2E = 1.4426950408889634;
+    // cooperative tile loads: K tile (64 keys × 64 d) and V tile, 2 × 16 B per thread each
+    std::string kbase = std::to_string(P.kacc.addr.c0) + " + " + hterm(kc, kh, khc);
+    std::string vbase = std::to_string(P.vacc.addr.c0) + " + " + hterm(vc, vh, vhc);
+    k.line("sanic_u32x4 kreg[2], vreg[2];");
+    auto load_tile = [&](Code& c2, const std::string& t0) {
+        c2.line("#pragma unroll");
+        c2.line("for (int u = 0; u < 2; ++u) {");
+        c2.line("  const int ch = tid + u * 256;");           // 512 chunks of 8 bf16
+        c2.line("  const int r = ch >> 3, c8 = (ch & 7) * 8;");
+        c2.line("  kreg[u] = *(const sanic_u32x4*)(" + kp + " + " + kbase + " + (" + t0 + " + r) * " + std::to_string(kc[1]) + " + c8);");
+        if (v_rows)
+            c2.line("  vreg[u] = *(const sanic_u32x4*)(" + vp + " + " + vbase + " + (" + t0 + " + r) * " + std::to_string(vc[1]) + " + c8);");
+        else   // V^T in memory: row = e, 8 consecutive keys
+            c2.line("  vreg[u] = *(const sanic_u32x4*)(" + vp + " + " + vbase + " + (idx_t)r * " + std::to_string(vc[2]) + " + " + t0 + " + c8);");
+        c2.line("}");
+    };
+    auto store_tile = [&](Code& c2, const std::string& buf) {
+        c2.line("#pragma unroll");
+        c2.line("for (int u = 0; u < 2; ++u) {");
+        c2.line("  const int ch = tid + u * 256;");
+        c2.line("  const int r = ch >> 3, c8 = (ch & 7) * 8;");
+        c2.line("  *(sanic_u32x4*)(&k_lds[" + buf + "][r * " + std::to_string(KS) + " + c8]) = kreg[u];");
+        if (v_rows) {
+            // transpose into V^T[e][key]
+            c2.line("  #pragma unroll");
+            c2.line("  for (int j = 0; j < 8; ++j) v_lds[" + buf + "][(c8 + j) * " + std::to_string(VS) + " + r] = (unsigned short)(vreg[u][j >> 1] >> (16 * (j & 1)));");
+        } else {
+            c2.line("  *(sanic_u32x4*)(&v_lds[" + buf + "][r * " + std::to_string(VS) + " + c8]) = vreg[u];");
+        }
+        c2.line("}");
+    };
+    k.line("if (klo < khi) {");
+    k.indent++;
+    load_tile(k, "klo");
+    store_tile(k, "0");
+    k.line("__syncthreads();");
+    k.line("int buf = 0;");
+    k.line("for (idx_t t0 = klo; t0 < khi; t0 += 64) {");
+    k.indent++;
+    k.line("const bool more = t0 + 64 < khi;");
+    k.line("if (more) {");
+    k.indent++;
+    load_tile(k, "(t0 + 64)");
+    k.indent--;
+    k.line("}");
+    k.line("const bool live = t0 < whi && t0 + 64 > wlo;");       // some row of this wave sees the tile
+    k.line("if (live) {");
+    k.indent++;
+    k.line("const bool full = t0 >= flo && t0 + 64 <= fhi;");     // every row sees all of it
+    // S^T tiles: kt (16 keys) × qt (16 queries), contraction over d in 2 steps of 32
+    k.line("f32x4 s[4][2];");
+    k.line("#pragma unroll");
+    k.line("for (int kt = 0; kt < 4; ++kt) {");
+    k.line("  s[kt][0] = (f32x4){0, 0, 0, 0}; s[kt][1] = (f32x4){0, 0, 0, 0};");
+    k.line("  #pragma unroll");
+    k.line("  for (int ds = 0; ds < 2; ++ds) {");
+    k.line("    const bf16x8 ka = *(const bf16x8*)(&k_lds[buf][(kt * 16 + l16) * " + std::to_string(KS) + " + ds * 32 + lq * 8]);");
+    k.line("    s[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[0][ds], s[kt][0], 0, 0, 0);");
+    k.line("    s[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[1][ds], s[kt][1], 0, 0, 0);");
+    k.line("  }");
+    k.line("}");
+    // online softmax per query column (lane-local, max reduced across the 4 lane groups)
+    k.line("bf16x8 pf[2][2];");
+    k.line("#pragma unroll");
+    k.line("for (int qt = 0; qt < 2; ++qt) {");
+    k.indent++;
+    k.line("const idx_t qi = q0 + qt * 16 + l16;");
+    k.line("float sv[16];");
+    k.line("if (full) {");
+    k.line("  #pragma unroll");
+    k.line("  for (int kt = 0; kt < 4; ++kt)");
+    k.line("    #pragma unroll");
+    k.line("    for (int r = 0; r < 4; ++r) sv[kt * 4 + r] = score_full(a, s[kt][qt][r], hh, qi, t0 + kt * 16 + lq * 4 + r);");
+    k.line("} else {");
+    k.line("  #pragma unroll");
+    k.line("  for (int kt = 0; kt < 4; ++kt)");
+    k.line("    #pragma unroll");
+    k.line("    for (int r = 0; r < 4; ++r) sv[kt * 4 + r] = score_part(a, s[kt][qt][r], hh, qi, t0 + kt * 16 + lq * 4 + r);");
+    k.line("}");
+    k.line("float mt = sv[0];");
+    k.line("#pragma unroll");
+    k.line("for (int i = 1; i < 16; ++i) mt = fmaxf(mt, sv[i]);");
+    k.line("mt = fmaxf(mt, __shfl_xor(mt, 16, 64));");
+    k.line("mt = fmaxf(mt, __shfl_xor(mt, 32, 64));");
+    k.line("const float mn = fmaxf(m_run[qt], mt);");
+    // the carrier's guarded rescale: a side whose max is −∞ weighs 0
+    k.line("const float alpha = m_run[qt] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - mn) * " + flit(LOG2E) + ");");
+    // (s − m) first, then the log2(e) scale: with masked scores near −1e30 a fused
+    // s·log2e − m·log2e does not cancel exactly and exp2 would overflow
+    k.line("float ps = 0.0f;");
+    k.line("unsigned short pb[16];");
+    k.line("#pragma unroll");
+    k.line("for (int i = 0; i < 16; ++i) {");
+    k.line("  const float p = mn == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((sv[i] - mn) * " + flit(LOG2E) + ");");
+    k.line("  ps += p;");
+    k.line("  pb[i] = sanic_to_bf16(p);");
+    k.line("}");
+    k.line("l_run[qt] = l_run[qt] * alpha + ps;");
+    k.line("m_run[qt] = mn;");
+    k.line("#pragma unroll");
+    k.line("for (int dt = 0; dt < 4; ++dt) { o[dt][qt][0] *= alpha; o[dt][qt][1] *= alpha; o[dt][qt][2] *= alpha; o[dt][qt][3] *= alpha; }");
+    // P^T as the B operand for key step ks: slots 0..3 = keys 32ks + lq·4 + r (tile 2ks),
+    // slots 4..7 = keys 32ks + 16 + lq·4 + r (tile 2ks+1)
+    k.line("#pragma unroll");
+    k.line("for (int ks = 0; ks < 2; ++ks)");
+    k.line("  #pragma unroll");
+    k.line("  for (int j = 0; j < 8; ++j) pf[qt][ks][j] = (short)pb[(2 * ks + (j >> 2)) * 4 + (j & 3)];");
+    k.indent--;
+    k.line("}");
+    // O^T += V^T · P^T ; V^T A operand: row e = dt·16 + l16, keys in the same slot order
+    k.line("#pragma unroll");
+    k.line("for (int dt = 0; dt < 4; ++dt)");
+    k.line("  #pragma unroll");
+    k.line("  for (int ks = 0; ks < 2; ++ks) {");
+    k.line("    const unsigned short* vr = &v_lds[buf][(dt * 16 + l16) * " + std::to_string(VS) + " + ks * 32 + lq * 4];");
+    k.line("    const uint2 lo4 = *(const uint2*)(vr), hi4 = *(const uint2*)(vr + 16);");
+    k.line("    bf16x8 va;");
+    k.line("    va[0] = (short)(lo4.x & 0xFFFF); va[1] = (short)(lo4.x >> 16); va[2] = (short)(lo4.y & 0xFFFF); va[3] = (short)(lo4.y >> 16);");
+    k.line("    va[4] = (short)(hi4.x & 0xFFFF); va[5] = (short)(hi4.x >> 16); va[6] = (short)(hi4.y & 0xFFFF); va[7] = (short)(hi4.y >> 16);");
+    k.line("    o[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[0][ks], o[dt][0], 0, 0, 0);");
+    k.line("    o[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[1][ks], o[dt][1], 0, 0, 0);");
+    k.line("  }");
+    k.indent--;
+    k.line("}");
+    k.line("if (more) {");
+    k.indent++;
+    store_tile(k, "buf ^ 1");
+    k.indent--;
+    k.line("}");
+    k.line("__syncthreads();");
+    k.line("buf ^= 1;");
+    k.indent--;
+    k.line("}");
+    k.indent--;
+    k.line("}");
+    // finish: the row sum across the 4 lane groups, then project per output point
+    k.line("#pragma unroll");
+    k.line("for (int qt = 0; qt < 2; ++qt) {");
+    k.indent++;
+    k.line("float lt = l_run[qt];");
+    k.line("lt += __shfl_xor(lt, 16, 64);");
+    k.line("lt += __shfl_xor(lt, 32, 64);");
+    k.line("const idx_t qi = q0 + qt * 16 + l16;");
+    k.line("#pragma unroll");
+    k.line("for (int dt = 0; dt < 4; ++dt)");
+    k.line("  #pragma unroll");
+    k.line("  for (int r = 0; r < 4; ++r) {");
+    k.line("    float fs[" + std::to_string(c.slots) + "];");
+    k.line("    fs[" + std::to_string(P.max_slot) + "] = m_run[qt];");
+    for (size_t s = 0; s < P.scalar_slots.size(); s++)
+        k.line("    fs[" + std::to_string(P.scalar_slots[s]) + "] = " + flit(P.scalar_into[s]) + " * lt;");
+    k.line("    fs[" + std::to_string(P.vec_slots[0]) + "] = o[dt][qt][r];");
+    k.line("    finish(a, fs, hh, qi, dt * 16 + lq * 4 + r);");
+    k.line("  }");
+    k.indent--;
+    k.line("}");
+
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
+    out.kernel_kind = "skeleton:flash_prefill[rep " + std::to_string(P.rep) + "]";
+    out.source = src.str();
+    out.launches.push_back({kname, "", dim3((unsigned)(NH * NQB)), dim3(256), 0, R.arg_list()});
+    return true;
+}
+
+}  // namespace sanic

@@ -824,6 +824,7 @@ bool lower_pointwise_skeleton(const sanic_program_desc* d, int si, int64_t&, Low
 }
 
 bool lower_skeleton(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
+    if (lower_flash_prefill(d, si, scratch, out)) return true;
     if (lower_attn_decode(d, si, scratch, out)) return true;
     return false;
 }
