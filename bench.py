@@ -101,13 +101,141 @@ def cpu_baseline(shape, seconds_budget=20.0):
                       f"{os.uname().nodename})"}
 
 
+# ── secondary configurations (BASELINE.json configs B, C, D): one dominant kernel each ──
+
+CONFIGS = {
+    # name: (algorithmic unit count, unit, bound)
+    "B1": "RMSNorm-fused GEMV M=1, K=2048 → N=8192, W bf16 [K, N] (K-major)",
+    "B1rows": "RMSNorm-fused GEMV M=1, K=2048 → N=8192, W bf16 [N, K] (the reference's [out, in])",
+    "B2": "RMSNorm-fused GEMM M=512, K=2048 → N=8192, W bf16 [K, N]",
+    "C1": "GQA causal FlashAttention prefill, 32/8 heads, d=64, S=4096 (RoPE'd Q/K)",
+    "C2": "GQA sliding-window (1024) FlashAttention prefill, 32/8 heads, d=64, S=4096",
+    "C3": "GQA decode attention, 1 query vs 4096-entry KV cache, split-K combine",
+    "D1": "int4 group-quantized GEMV M=1, [8192, 2048] uint4, group 64",
+    "D2": "int4 group-quantized GEMM M=128, [8192, 2048] uint4, group 64",
+}
+
+
+def _bind_random(dev, prog, keep, seed=7):
+    """Device-resident synthetic inputs for every INPUT/STATE buffer of `prog` (torch RNG)."""
+    import torch
+    from sanic_amd import ir
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    binds = {}
+    for b in prog.buffers:
+        if b.role not in (0, 1):
+            continue
+        n = int(__import__("math").prod(b.shape)) if b.shape else 1
+        if b.dtype == ir.BF16:
+            t = torch.randn(n, generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+            if b.name in ("S", "Z"):
+                t = (t.float().abs() * 0.005 + 0.001).to(torch.bfloat16)
+        elif b.dtype == ir.F32:
+            t = torch.zeros(max(n, 1), device="cuda", dtype=torch.float32)
+            if b.name == "position":
+                t.fill_(4095.0)
+        elif b.dtype in (ir.U4, ir.I4):
+            t = torch.randint(0, 256, ((n + 1) // 2,), generator=g, device="cuda", dtype=torch.uint8)
+        else:
+            t = torch.zeros(b.nbytes, device="cuda", dtype=torch.uint8)
+        keep.append(t)
+        binds[b.name] = dev.wrap(t.data_ptr(), b.nbytes)
+    torch.cuda.synchronize()
+    return binds
+
+
+def _time_program(dev, prog, keep, reps=20):
+    exe = dev.prepare(prog)
+    binds = _bind_random(dev, prog, keep)
+    rp = exe.capture(binds)
+    rp.step_many(3)
+    return rp.step_many(reps) / reps, exe
+
+
+def bench_config(name: str, copies: int = 8):
+    from sanic_amd import configs
+    from sanic_amd.backend import HipDevice
+    dev = HipDevice(0)
+    keep = []
+    if name in ("B1", "B1rows", "B2"):
+        M = 512 if name == "B2" else 1
+        mk = lambda: configs.rmsnorm_projection(M=M, kmajor=(name != "B1rows"))
+        main, K, N = 0, 2048, 8192
+        flops = 2.0 * M * K * N + 2.0 * M * K
+        nbytes = K * N * 2 + M * K * 2 + K * 2 + M * N * 2
+        bound = "mfma" if name == "B2" else "hbm"
+    elif name in ("D1", "D2"):
+        M = 128 if name == "D2" else 1
+        mk = lambda: configs.int4_matmul(M=M)
+        main, K, N = 0, 2048, 8192
+        flops = 2.0 * M * K * N
+        nbytes = N * K // 2 + 2 * (N * K // 64) * 2 + M * K * 2 + M * N * 2
+        bound = "hbm" if name == "D1" else "both"
+    elif name in ("C1", "C2"):
+        w = 1024 if name == "C2" else 0
+        mk = lambda: configs.flash_prefill(window=w, rope_stages=False)
+        main = 0
+        S, NH, HD = 4096, 32, 64
+        if w:
+            pairs = w * (w + 1) / 2 + (S - w) * w
+        else:
+            pairs = S * (S + 1) / 2
+        flops = 4.0 * HD * NH * pairs
+        nbytes = 2 * (NH * S * HD * 2) + 2 * (8 * S * HD * 2)
+        bound = "mfma"
+    elif name == "C3":
+        mk = lambda: configs.decode_attention()
+        main = 0
+        flops = 4.0 * 64 * 32 * 4096
+        nbytes = 2 * 8 * 4096 * 64 * 2
+        bound = "hbm"
+    else:
+        raise SystemExit(f"unknown config {name}; known: {sorted(CONFIGS)}")
+    # end-to-end: the configuration's whole program (for C1/C2 with the RoPE stages)
+    full = configs.flash_prefill(window=(1024 if name == "C2" else 0)) if name in ("C1", "C2") else mk()
+    t_full, exe_full = _time_program(dev, full, keep)
+    # the dominant kernel alone, `copies` launches per replay
+    prog = mk()
+    prog.repeat_stage(main, copies - 1)
+    import os as _os
+    _os.environ["SANIC_HIP_NO_BATCH"] = "1"
+    t_k, exe = _time_program(dev, prog, keep)
+    del _os.environ["SANIC_HIP_NO_BATCH"]
+    per = t_k / copies
+    kind = exe.stage_kernel(main)
+    roof = {"bound": bound, "kernel": kind, "us_per_launch": per * 1e6, "traffic": None}
+    if bound in ("hbm", "both"):
+        roof.update({"achieved": nbytes / per / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": nbytes / per / HBM_PEAK})
+    if bound in ("mfma", "both"):
+        key = "achieved" if bound == "mfma" else "achieved_tflops"
+        roof.update({key: flops / per / 1e12})
+        if bound == "mfma":
+            roof.update({"peak": 2500.0, "unit": "TFLOP/s", "frac": flops / per / 2.5e15})
+        else:
+            roof.update({"frac_mfma": flops / per / 2.5e15})
+    out = {"metric": f"{name}: {CONFIGS[name]}", "value": (flops / t_full / 1e12) if bound == "mfma" else (nbytes / t_full / 1e9),
+           "unit": "TFLOP/s" if bound == "mfma" else "GB/s", "n_gpus": 1, "config": {"workload": CONFIGS[name]},
+           "ms_end_to_end": t_full * 1e3, "stages": [exe_full.stage_kernel(i) for i in range(len(full.stages))],
+           "roofline": roof, "flops": flops, "bytes": nbytes, "dtype": "bf16"}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--config", default=None, help="measure a secondary configuration instead: " + ", ".join(CONFIGS))
     args = ap.parse_args()
+    if args.config:
+        import torch
+        torch.cuda.init()
+        for name in args.config.split(","):
+            bench_config(name)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
                                    "(see the sharding design note)", "n_gpus": args.gpus}))

@@ -207,6 +207,32 @@ bool flash_plan(const sanic_program_desc* d, int si, FlashPlan& P) {
     return true;
 }
 
+// On tiles every row sees entirely, the score must be `dot · c` (the additive mask terms are
+// zero there): read c off the leaf so the tile can fold the scale into the exp2 argument.
+bool full_score_scale(const sanic_program_desc* d, int node, int dot, const std::vector<WindowBound>& win, double& c) {
+    const sanic_node& n = d->nodes[node];
+    if (node == dot) { c = 1.0; return true; }
+    if (n.kind != SANIC_NODE_MAP) return false;
+    if (n.op == SANIC_OP_ADD) {
+        for (int k = 0; k < 2; k++)
+            for (auto& w : win)
+                if (n.in[k] == w.where_node) return full_score_scale(d, n.in[1 - k], dot, win, c);
+        return false;
+    }
+    if (n.op == SANIC_OP_MUL) {
+        for (int k = 0; k < 2; k++) {
+            const sanic_node& o = d->nodes[n.in[1 - k]];
+            if (o.kind == SANIC_NODE_CONST && o.rank == 0) {
+                double inner;
+                if (!full_score_scale(d, n.in[k], dot, win, inner)) return false;
+                c = inner * o.value;
+                return true;
+            }
+        }
+    }
+    return false;
+}
+
 }  // namespace
 
 bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
@@ -253,6 +279,8 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     std::string entry_full = Rf.entry();
     for (int b : Rs.bufs) R.param(b);
     for (int b : Rf.bufs) R.param(b);
+    double scale_c = 0.0;
+    const bool scale_known = full_score_scale(d, st.leaf[P.sleaf], P.dot_reduce, win, scale_c) && scale_c > 0.0;
 
     // window edges per query row (for tile skipping / full-tile detection)
     Code wc;
@@ -301,9 +329,25 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     src << "typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;\n";
     src << "typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;\n";
     src << R.args_struct({});
-    src << "__device__ __forceinline__ float score_part(const Args& a, float dotv, idx_t hh, idx_t qi, idx_t kj) {\n"
+    src << "typedef __bf16 sanic_bf16x2 __attribute__((ext_vector_type(2)));\n";
+    src << "typedef float sanic_f32x2 __attribute__((ext_vector_type(2)));\n";
+    src << "__device__ __forceinline__ unsigned pk_bf16(float x, float y) {\n"
+           "  return __builtin_bit_cast(unsigned, __builtin_convertvector((sanic_f32x2){x, y}, sanic_bf16x2));\n}\n";
+    // max across the 4 lane groups of a query column (lanes l, l^16, l^32, l^48): gfx950
+    // permlane swaps, no LDS round trip
+    src << "__device__ __forceinline__ float wave_max_x4(float v) {\n"
+           "  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);\n"
+           "  v = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));\n"
+           "  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);\n"
+           "  return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));\n}\n";
+    src << "__device__ __forceinline__ float wave_sum_x4(float v) {\n"
+           "  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);\n"
+           "  v = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);\n"
+           "  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);\n"
+           "  return __uint_as_float(r16[0]) + __uint_as_float(r16[1]);\n}\n";
+    src << "__device__ __forceinline__ float score_part(const Args& a, float dotv, int hh, int qi, int kj) {\n"
         << entry_part << sp.str() << "  return " << vpart << ";\n}\n";
-    src << "__device__ __forceinline__ float score_full(const Args& a, float dotv, idx_t hh, idx_t qi, idx_t kj) {\n"
+    src << "__device__ __forceinline__ float score_full(const Args& a, float dotv, int hh, int qi, int kj) {\n"
         << entry_full << sf.str() << "  return " << vfull << ";\n}\n";
     src << "__device__ __forceinline__ void window(const Args& a, idx_t hh, idx_t qrow, idx_t& lo, idx_t& hi) {\n"
         << Rw.entry() << wc.str() << "  lo = wlo; hi = whi;\n}\n";
@@ -400,10 +444,11 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     load_tile(k, "(t0 + 64)");
     k.indent--;
     k.line("}");
-    k.line("const bool live = t0 < whi && t0 + 64 > wlo;");       // some row of this wave sees the tile
+    // wave-uniform tile classification (scalar branches)
+    k.line("const int live = __builtin_amdgcn_readfirstlane((int)(t0 < whi && t0 + 64 > wlo));");   // some row sees it
     k.line("if (live) {");
     k.indent++;
-    k.line("const bool full = t0 >= flo && t0 + 64 <= fhi;");     // every row sees all of it
+    k.line("const int full = __builtin_amdgcn_readfirstlane((int)(t0 >= flo && t0 + 64 <= fhi));");  // every row sees all
     // S^T tiles: kt (16 keys) × qt (16 queries), contraction over d in 2 steps of 32
     k.line("f32x4 s[4][2];");
     k.line("#pragma unroll");
@@ -416,54 +461,93 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("    s[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[1][ds], s[kt][1], 0, 0, 0);");
     k.line("  }");
     k.line("}");
-    // online softmax per query column (lane-local, max reduced across the 4 lane groups)
-    k.line("bf16x8 pf[2][2];");
+    // online softmax per query column (lane-local; the max reduces across the 4 lane groups)
+    k.line("sanic_u32x4 pw[2][2];");
     k.line("#pragma unroll");
     k.line("for (int qt = 0; qt < 2; ++qt) {");
     k.indent++;
-    k.line("const idx_t qi = q0 + qt * 16 + l16;");
+    k.line("const int qi = (int)(q0 + qt * 16 + l16);");
+    k.line("const int kb = (int)t0 + lq * 4;");
     k.line("float sv[16];");
-    k.line("if (full) {");
+    k.line("float p[16];");
+    k.line("float mn, alpha;");
+    if (scale_known) {
+        // full tiles: score = dot·c, so max and exp2 work on the raw dot (c > 0)
+        k.line("if (full) {");
+        k.indent++;
+        k.line("float mt = fmaxf(fmaxf(s[0][qt][0], s[0][qt][1]), fmaxf(s[0][qt][2], s[0][qt][3]));");
+        k.line("#pragma unroll");
+        k.line("for (int kt = 1; kt < 4; ++kt) mt = fmaxf(mt, fmaxf(fmaxf(s[kt][qt][0], s[kt][qt][1]), fmaxf(s[kt][qt][2], s[kt][qt][3])));");
+        k.line("mt = wave_max_x4(mt) * " + flit(scale_c) + ";");
+        k.line("mn = fmaxf(m_run[qt], mt);");
+        k.line("alpha = m_run[qt] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - mn) * " + flit(LOG2E) + ");");
+        k.line("if (__all(mn > -1e29f)) {");
+        k.line("  const float mb = mn * " + flit(LOG2E) + ";");
+        k.line("  #pragma unroll");
+        k.line("  for (int kt = 0; kt < 4; ++kt)");
+        k.line("    #pragma unroll");
+        k.line("    for (int r = 0; r < 4; ++r) p[kt * 4 + r] = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][r], " + flit(scale_c * LOG2E) + ", -mb));");
+        k.line("} else {");
+        k.line("  #pragma unroll");
+        k.line("  for (int kt = 0; kt < 4; ++kt)");
+        k.line("    #pragma unroll");
+        k.line("    for (int r = 0; r < 4; ++r) p[kt * 4 + r] = mn == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((s[kt][qt][r] * " + flit(scale_c) + " - mn) * " + flit(LOG2E) + ");");
+        k.line("}");
+        k.indent--;
+        k.line("} else {");
+        k.indent++;
+    } else {
+        k.line("{");
+        k.indent++;
+    }
+    // partial tiles (and scores of any other shape): the rendered leaf per element
+    k.line("#pragma unroll");
+    k.line("for (int kt = 0; kt < 4; ++kt)");
     k.line("  #pragma unroll");
-    k.line("  for (int kt = 0; kt < 4; ++kt)");
-    k.line("    #pragma unroll");
-    k.line("    for (int r = 0; r < 4; ++r) sv[kt * 4 + r] = score_full(a, s[kt][qt][r], hh, qi, t0 + kt * 16 + lq * 4 + r);");
+    k.line("  for (int r = 0; r < 4; ++r) sv[kt * 4 + r] = full ? score_full(a, s[kt][qt][r], (int)hh, qi, kb + kt * 16 + r)"
+           " : score_part(a, s[kt][qt][r], (int)hh, qi, kb + kt * 16 + r);");
+    k.line("float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));");
+    k.line("#pragma unroll");
+    k.line("for (int i = 4; i < 16; i += 2) mt = fmaxf(mt, fmaxf(sv[i], sv[i + 1]));");
+    k.line("mt = wave_max_x4(mt);");
+    k.line("mn = fmaxf(m_run[qt], mt);");
+    // the carrier's guarded rescale: a side whose max is −∞ weighs 0
+    k.line("alpha = m_run[qt] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - mn) * " + flit(LOG2E) + ");");
+    // Fast form exp2(s·log2e − m·log2e) (one FMA) while every row of the wave has a moderate
+    // max; when some row's max is a masked score (≈ −1e30) or −∞ the fused form does not
+    // cancel exactly, so (s − m)·log2e is used for that tile.
+    k.line("if (__all(mn > -1e29f)) {");
+    k.line("  const float mb = mn * " + flit(LOG2E) + ";");
+    k.line("  #pragma unroll");
+    k.line("  for (int i = 0; i < 16; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], " + flit(LOG2E) + ", -mb));");
     k.line("} else {");
     k.line("  #pragma unroll");
-    k.line("  for (int kt = 0; kt < 4; ++kt)");
-    k.line("    #pragma unroll");
-    k.line("    for (int r = 0; r < 4; ++r) sv[kt * 4 + r] = score_part(a, s[kt][qt][r], hh, qi, t0 + kt * 16 + lq * 4 + r);");
+    k.line("  for (int i = 0; i < 16; ++i) p[i] = mn == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((sv[i] - mn) * " + flit(LOG2E) + ");");
     k.line("}");
-    k.line("float mt = sv[0];");
-    k.line("#pragma unroll");
-    k.line("for (int i = 1; i < 16; ++i) mt = fmaxf(mt, sv[i]);");
-    k.line("mt = fmaxf(mt, __shfl_xor(mt, 16, 64));");
-    k.line("mt = fmaxf(mt, __shfl_xor(mt, 32, 64));");
-    k.line("const float mn = fmaxf(m_run[qt], mt);");
-    // the carrier's guarded rescale: a side whose max is −∞ weighs 0
-    k.line("const float alpha = m_run[qt] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - mn) * " + flit(LOG2E) + ");");
-    // (s − m) first, then the log2(e) scale: with masked scores near −1e30 a fused
-    // s·log2e − m·log2e does not cancel exactly and exp2 would overflow
-    k.line("float ps = 0.0f;");
-    k.line("unsigned short pb[16];");
-    k.line("#pragma unroll");
-    k.line("for (int i = 0; i < 16; ++i) {");
-    k.line("  const float p = mn == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((sv[i] - mn) * " + flit(LOG2E) + ");");
-    k.line("  ps += p;");
-    k.line("  pb[i] = sanic_to_bf16(p);");
-    k.line("}");
-    k.line("l_run[qt] = l_run[qt] * alpha + ps;");
-    k.line("m_run[qt] = mn;");
-    k.line("#pragma unroll");
-    k.line("for (int dt = 0; dt < 4; ++dt) { o[dt][qt][0] *= alpha; o[dt][qt][1] *= alpha; o[dt][qt][2] *= alpha; o[dt][qt][3] *= alpha; }");
-    // P^T as the B operand for key step ks: slots 0..3 = keys 32ks + lq·4 + r (tile 2ks),
-    // slots 4..7 = keys 32ks + 16 + lq·4 + r (tile 2ks+1)
-    k.line("#pragma unroll");
-    k.line("for (int ks = 0; ks < 2; ++ks)");
-    k.line("  #pragma unroll");
-    k.line("  for (int j = 0; j < 8; ++j) pf[qt][ks][j] = (short)pb[(2 * ks + (j >> 2)) * 4 + (j & 3)];");
     k.indent--;
     k.line("}");
+    k.line("float ps = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));");
+    k.line("ps += ((p[8] + p[9]) + (p[10] + p[11])) + ((p[12] + p[13]) + (p[14] + p[15]));");
+    k.line("l_run[qt] = l_run[qt] * alpha + ps;");
+    k.line("m_run[qt] = mn;");
+    k.line("if (!__all(alpha == 1.0f)) {");   // the running max moved for some row: rescale
+    k.line("  #pragma unroll");
+    k.line("  for (int dt = 0; dt < 4; ++dt) { o[dt][qt][0] *= alpha; o[dt][qt][1] *= alpha; o[dt][qt][2] *= alpha; o[dt][qt][3] *= alpha; }");
+    k.line("}");
+    // P^T as the B operand for key step ks: slots 0..3 = keys 32ks + lq·4 + r (tile 2ks),
+    // slots 4..7 = keys 32ks + 16 + lq·4 + r (tile 2ks+1); two slots per dword, RNE in hardware
+    k.line("#pragma unroll");
+    k.line("for (int ks = 0; ks < 2; ++ks) {");
+    k.line("  pw[qt][ks].x = pk_bf16(p[8 * ks + 0], p[8 * ks + 1]);");
+    k.line("  pw[qt][ks].y = pk_bf16(p[8 * ks + 2], p[8 * ks + 3]);");
+    k.line("  pw[qt][ks].z = pk_bf16(p[8 * ks + 4], p[8 * ks + 5]);");
+    k.line("  pw[qt][ks].w = pk_bf16(p[8 * ks + 6], p[8 * ks + 7]);");
+    k.line("}");
+    k.indent--;
+    k.line("}");
+    k.line("bf16x8 pf[2][2];");
+    k.line("#pragma unroll");
+    k.line("for (int qt = 0; qt < 2; ++qt) { pf[qt][0] = __builtin_bit_cast(bf16x8, pw[qt][0]); pf[qt][1] = __builtin_bit_cast(bf16x8, pw[qt][1]); }");
     // O^T += V^T · P^T ; V^T A operand: row e = dt·16 + l16, keys in the same slot order
     k.line("#pragma unroll");
     k.line("for (int dt = 0; dt < 4; ++dt)");
@@ -495,8 +579,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("for (int qt = 0; qt < 2; ++qt) {");
     k.indent++;
     k.line("float lt = l_run[qt];");
-    k.line("lt += __shfl_xor(lt, 16, 64);");
-    k.line("lt += __shfl_xor(lt, 32, 64);");
+    k.line("lt = wave_sum_x4(lt);");
     k.line("const idx_t qi = q0 + qt * 16 + l16;");
     k.line("#pragma unroll");
     k.line("for (int dt = 0; dt < 4; ++dt)");
@@ -512,7 +595,8 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.indent--;
     k.line("}");
 
-    src << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
+    // two waves per SIMD: at most 256 VGPRs, so MFMA of one wave overlaps the softmax of the other
+    src << "extern \"C\" __global__ void __launch_bounds__(256, 2) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     out.kernel_kind = "skeleton:flash_prefill[rep " + std::to_string(P.rep) + "]";
     out.source = src.str();
     out.launches.push_back({kname, "", dim3((unsigned)(NH * NQB)), dim3(256), 0, R.arg_list()});

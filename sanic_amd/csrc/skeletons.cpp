@@ -572,7 +572,8 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
     std::string ws0 = wshape(P0, wb0, wd0);
     std::set<int> written{d->stages[si].out_buffer};
     std::vector<std::vector<int>> seg_wbufs{wb0};
-    for (int s = si + 1; s < d->n_stages && group.size() < 8; s++) {
+    const bool no_batch = getenv("SANIC_HIP_NO_BATCH") != nullptr;   // measurement knob
+    for (int s = si + 1; s < d->n_stages && group.size() < 8 && !no_batch; s++) {
         GemvPlan P;
         if (!gemv_plan(d, s, P) || P.K != P0.K || P.cslots.size() != P0.cslots.size() || P.rslots.size() != P0.rslots.size())
             break;

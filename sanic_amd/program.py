@@ -120,6 +120,22 @@ class Program:
         self.stages.append(Stage(1, name, out, grid, value=value, where=where))
         return self.node(out.name)
 
+    def repeat_stage(self, i: int, copies: int) -> List[str]:
+        """Append `copies` more instances of stage `i`, each writing its own output buffer
+        (for timing one kernel as back-to-back launches inside one captured graph)."""
+        import copy as _copy
+        st = self.stages[i]
+        names = []
+        for r in range(copies):
+            name = f"{st.out.name}.copy{r}"
+            out = self._decl(name, OUTPUT, st.out.shape, st.out.dtype)
+            dup = _copy.copy(st)
+            dup.out = out
+            dup.name = name
+            self.stages.append(dup)
+            names.append(name)
+        return names
+
     # ── serialization ──
     def pack(self):
         """Return (ProgramDesc, keepalive) for the C ABI."""
