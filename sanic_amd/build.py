@@ -6,7 +6,7 @@ import subprocess
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-SOURCES = ["runtime.cpp", "emit_hip.cpp", "skeletons.cpp", "skel_attention.cpp", "skel_flash.cpp", "rtc.cpp"]
+SOURCES = ["runtime.cpp", "emit_hip.cpp", "skeletons.cpp", "skel_attention.cpp", "skel_flash.cpp", "skel_gemm.cpp", "rtc.cpp"]
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", "--offload-arch=gfx950",
          # packed-f32 instruction forms stay disabled for device code
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

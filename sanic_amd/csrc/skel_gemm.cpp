@@ -1,0 +1,451 @@
+// GEMM skeleton: Plain(Add) carriers with two output axes (rows m from the row leaves, columns
+// n from the weight leaf) on bf16 MFMA (v_mfma_f32_16x16x32_bf16) — the RMSNorm-fused projection
+// at prefill sizes and the int4 group-quantized matmul (configs B2/D2), i.e. the gemv carriers
+// of skeletons.cpp when M is large enough to be a real contraction.
+//
+// Structure required: every slot Plain(Add); one weight leaf binding (n, stream); row leaves
+// binding (m, stream) or (stream); each slot's `into` is either W·rest(row items) (a contraction
+// slot: A = rest, B = W, both rounded to bf16 for the MFMA) or free of W (a row slot: Σx² of a
+// fused RMSNorm, folded per row in f32 alongside the A tile).
+//
+// Kernel shape: workgroup tile BM × BN (4 waves in 2 × 2, each (BM/2) × (BN/2) of 16×16 MFMA
+// tiles), K in 64-wide steps, A and B tiles double-buffered in LDS with k contiguous so every
+// MFMA operand is one ds_read_b128; the weight leaf is loaded by the vector renderer (128-bit
+// runs of 8 along k, per-group scale/zero once per run, packed nibbles decoded in registers);
+// project, epilogue and the narrowing store per output element.
+#include <algorithm>
+#include <cmath>
+#include <functional>
+#include <set>
+
+#include "emit.h"
+#include "skeletons.h"
+
+namespace sanic {
+
+namespace {
+
+struct GemmPlan {
+    int mdim = -1, ndim = -1;
+    int64_t M = 0, N = 0, K = 0;
+    int w = -1;
+    std::vector<int> rows;          // row leaves
+    std::vector<int> cslots, rslots;
+};
+
+bool expr_reads(const sanic_program_desc* d, int e, int item) {
+    const sanic_expr& x = d->exprs[e];
+    if (x.op == SANIC_EX_ITEM) return x.index == item;
+    if (x.op >= SANIC_EX_CONST) return false;
+    for (int c : {x.a, x.b, x.c}) if (c >= 0 && expr_reads(d, c, item)) return true;
+    return false;
+}
+
+bool linear_mul(const sanic_program_desc* d, int e, int w) {
+    const sanic_expr& x = d->exprs[e];
+    if (x.op == SANIC_EX_ITEM) return x.index == w;
+    if (x.op == SANIC_OP_MUL) {
+        bool a = expr_reads(d, x.a, w), b = expr_reads(d, x.b, w);
+        if (a == b) return false;
+        return a ? linear_mul(d, x.a, w) : linear_mul(d, x.b, w);
+    }
+    return false;
+}
+
+// Render an Expr with item w read as 1 and items named by `item(i)`.
+std::string expr_rest(Renderer& R, Code& code, int e, int w, const std::function<std::string(int)>& item) {
+    const sanic_expr& x = R.d->exprs[e];
+    if (x.op == SANIC_EX_ITEM) return x.index == w ? "1.0f" : item(x.index);
+    if (x.op == SANIC_EX_CONST) return flit(x.value);
+    std::string s[3];
+    int kids[3] = {x.a, x.b, x.c};
+    for (int k = 0; k < 3; k++) if (kids[k] >= 0) s[k] = expr_rest(R, code, kids[k], w, item);
+    std::string out = R.fresh("e");
+    code.line("const float " + out + " = " + map_expr(x.op, s[0], s[1], s[2]) + ";");
+    return out;
+}
+
+bool gemm_plan(const sanic_program_desc* d, int si, GemmPlan& P) {
+    const sanic_stage& st = d->stages[si];
+    if (st.kind != SANIC_STAGE_FUSED) return false;
+    const sanic_carrier& c = st.carrier;
+    for (int k = 0; k < c.slots; k++)
+        if (c.kind[k].kind != SANIC_SLOT_PLAIN || c.kind[k].monoid != SANIC_MON_ADD) return false;
+    std::vector<int> big;
+    for (int j = 0; j < st.rank; j++) if (st.grid[j] > 1) big.push_back(j);
+    if (big.size() != 2 || st.stream % 64) return false;
+    P = GemmPlan();
+    P.K = st.stream;
+    // leaves bound to a big grid dim (plus the stream); the rest depend on the stream only
+    std::vector<std::pair<int, int>> dimmed;   // (leaf, dim)
+    std::vector<int> free_rows;
+    for (int l = 0; l < st.n_leaves; l++) {
+        const sanic_node& ln = d->nodes[st.leaf[l]];
+        std::set<int> dims;
+        bool has_s = false;
+        for (int j = 0; j < ln.rank; j++) {
+            int b = st.bind[l][j];
+            if (b == SANIC_BIND_STREAM) has_s = true;
+            else if (b >= 0 && st.grid[b] > 1) dims.insert(b);
+        }
+        if (dims.size() > 1 || !has_s) return false;
+        if (dims.empty()) free_rows.push_back(l);
+        else dimmed.push_back({l, *dims.begin()});
+    }
+    // the weight is the one dim-bound leaf that every row slot ignores and every other slot
+    // multiplies in exactly once; all other dim-bound leaves share the other (row) dim
+    for (auto& cand : dimmed) {
+        GemmPlan Q = P;
+        Q.w = cand.first;
+        Q.ndim = cand.second;
+        bool good = true;
+        for (auto& o : dimmed) {
+            if (o.first == cand.first) continue;
+            if (o.second == Q.ndim || (Q.mdim >= 0 && o.second != Q.mdim)) { good = false; break; }
+            Q.mdim = o.second;
+            Q.rows.push_back(o.first);
+        }
+        if (!good || Q.mdim < 0) continue;
+        for (int l : free_rows) Q.rows.push_back(l);
+        for (int k = 0; k < c.slots && good; k++) {
+            if (!expr_reads(d, c.into[k], Q.w)) Q.rslots.push_back(k);
+            else if (linear_mul(d, c.into[k], Q.w)) Q.cslots.push_back(k);
+            else good = false;
+        }
+        if (good && Q.cslots.size() == 1) { P = Q; break; }
+    }
+    if (P.w < 0) return false;
+    P.M = st.grid[P.mdim];
+    P.N = st.grid[P.ndim];
+    if (P.cslots.size() != 1) return false;
+    if (P.M < 64 || P.M % 64 || P.N % 32) return false;
+    return true;
+}
+
+}  // namespace
+
+// the vector weight renderer lives in skeletons.cpp
+std::vector<std::string> render_weight_run(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
+                                           const std::vector<int64_t>& ext, Code& lc, Code& dc, const std::string& nn,
+                                           const std::string& k0, const std::string& sfx, std::vector<int>& bufs,
+                                           std::vector<int>& dtypes, bool& ok, bool& contiguous, std::string& raw_bf16);
+
+bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
+    (void)scratch;
+    GemmPlan P;
+    if (!gemm_plan(d, si, P)) return false;
+    const sanic_stage& st = d->stages[si];
+    const sanic_carrier& c = st.carrier;
+    const int64_t M = P.M, N = P.N, K = P.K;
+    const int BM = M % 128 == 0 ? 128 : 64;
+    int BN = 128;
+    while (BN > 32 && (M / BM) * (N / BN) < 256) BN /= 2;
+    if (N % BN) return false;
+    const int WM = BM / 2, WN = BN / 2;       // per-wave tile
+    const int MT = WM / 16, NT = WN / 16;
+    const int SR = (int)P.rslots.size();
+    const int AS = 64 + 8, BS = 64 + 8;       // LDS row strides (bf16)
+    // An operand that is not a bf16 input as stored (x·g, dequantized weights) goes to the MFMA
+    // as hi + lo bf16 pair (hi = rn(v), lo = rn(v − hi): 16 significant bits, exact for the
+    // product of two bf16 values), so products match an f32 evaluation; one extra MFMA each.
+    auto raw_bf16_input = [&](int leaf) {
+        const sanic_node& n = d->nodes[st.leaf[leaf]];
+        return n.kind == SANIC_NODE_INPUT && n.dtype == SANIC_BF16;
+    };
+    const bool splitB = !raw_bf16_input(P.w);
+    bool splitA = true;
+    {
+        const sanic_expr& e = d->exprs[c.into[P.cslots[0]]];
+        if (e.op == SANIC_OP_MUL) {
+            const sanic_expr& ea = d->exprs[e.a];
+            const sanic_expr& eb = d->exprs[e.b];
+            const sanic_expr* other = nullptr;
+            if (ea.op == SANIC_EX_ITEM && ea.index == P.w) other = &eb;
+            if (eb.op == SANIC_EX_ITEM && eb.index == P.w) other = &ea;
+            if (other && other->op == SANIC_EX_ITEM && raw_bf16_input(other->index)) splitA = false;
+        }
+    }
+
+    Renderer R(d);
+    // weight leaf vector form over vars {0: n, 1: k}
+    const sanic_node& wn = d->nodes[st.leaf[P.w]];
+    std::vector<Sym> cw(wn.rank);
+    for (int j = 0; j < wn.rank; j++) {
+        int b = st.bind[P.w][j];
+        cw[j] = b == SANIC_BIND_STREAM ? Sym::var(1) : b == P.ndim ? Sym::var(0) : Sym();
+    }
+    std::vector<int> wbufs, wdts;
+    bool ok = true, contig = true;
+    std::string raw;
+    {
+        Code l1, d1;
+        render_weight_run(d, st.leaf[P.w], cw, {N, K}, l1, d1, "nn", "k0", "_p", wbufs, wdts, ok, contig, raw);
+        if (!ok) return false;
+    }
+    // row leaves vector forms over vars {0: m, 1: k}
+    std::vector<std::vector<Sym>> crow;
+    for (int l : P.rows) {
+        const sanic_node& ln = d->nodes[st.leaf[l]];
+        std::vector<Sym> cr(ln.rank);
+        for (int j = 0; j < ln.rank; j++) {
+            int b = st.bind[l][j];
+            cr[j] = b == SANIC_BIND_STREAM ? Sym::var(1) : b == P.mdim ? Sym::var(0) : Sym();
+        }
+        std::vector<int> rb, rd;
+        bool rok = true, rc = true;
+        std::string rr;
+        Code l1, d1;
+        render_weight_run(d, st.leaf[l], cr, {M, K}, l1, d1, "mm", "k0", "_p", rb, rd, rok, rc, rr);
+        if (!rok || !rc) return false;
+        crow.push_back(cr);
+    }
+
+    Code k;
+    k.indent = 1;
+    k.line("__shared__ unsigned short a_lds[2][" + std::to_string(BM * AS) + "];");
+    k.line("__shared__ unsigned short b_lds[2][" + std::to_string(BN * BS) + "];");
+    if (splitA) k.line("__shared__ unsigned short a_lo[2][" + std::to_string(BM * AS) + "];");
+    if (splitB) k.line("__shared__ unsigned short b_lo[2][" + std::to_string(BN * BS) + "];");
+    if (SR) k.line("__shared__ float rs_lds[" + std::to_string(BM * SR) + "];");
+    k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
+    k.line("const int l16 = lane & 15, lq = lane >> 4;");
+    k.line("const idx_t nb = blockIdx.x % " + std::to_string(N / BN) + ", mb = blockIdx.x / " + std::to_string(N / BN) + ";");
+    k.line("const idx_t m0 = mb * " + std::to_string(BM) + ", n0 = nb * " + std::to_string(BN) + ";");
+    k.line("const int wm = (wv >> 1) * " + std::to_string(WM) + ", wn = (wv & 1) * " + std::to_string(WN) + ";");
+    k.line("f32x4 acc[" + std::to_string(MT) + "][" + std::to_string(NT) + "];");
+    k.line("#pragma unroll");
+    k.line("for (int i = 0; i < " + std::to_string(MT) + "; ++i)");
+    k.line("  #pragma unroll");
+    k.line("  for (int j = 0; j < " + std::to_string(NT) + "; ++j) acc[i][j] = (f32x4){0, 0, 0, 0};");
+    for (int i = 0; i < SR; i++) k.line("float racc" + std::to_string(i) + " = 0.0f;");
+
+    // A tile: BM rows × 64 k; thread t owns row (t·BM/256)… with 256/BM threads per row, each
+    // a contiguous run of 64·BM/256 k in runs of 8
+    const int TPR = 256 / BM;              // threads per row: 2 (BM 128) or 4 (BM 64)
+    const int RUNS_A = 64 / TPR / 8;       // runs of 8 per thread per tile
+    // B tile: BN n × 64 k = BN·8 runs; k-contiguous weights: 8 lanes per row (coalesced rows),
+    // else adjacent lanes take adjacent n
+    const int RUNS_B = BN * 8 / 256;
+    auto emit_loads = [&](Code& c2, const std::string& kt0, const std::string& sfx) {
+        // A runs
+        c2.line("const idx_t mm" + sfx + " = m0 + tid / " + std::to_string(TPR) + ";");
+        for (int r = 0; r < RUNS_A; r++) {
+            std::string k0 = "(" + kt0 + " + (tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8) + ")";
+            for (size_t li = 0; li < P.rows.size(); li++) {
+                std::vector<int> rb, rd;
+                bool rok = true, rc = true;
+                std::string rr;
+                Code l1, d1;
+                l1.indent = d1.indent = c2.indent;
+                auto vals = render_weight_run(d, st.leaf[P.rows[li]], crow[li], {M, K}, l1, d1, "mm" + sfx, k0,
+                                              "_a" + std::to_string(li) + "_" + std::to_string(r) + sfx, rb, rd, rok, rc, rr);
+                for (size_t b = 0; b < rb.size(); b++)
+                    c2.line("const " + std::string(ctype_of(rd[b])) + "* __restrict__ wb" + std::to_string(b) + "_a" + std::to_string(li) + "_" + std::to_string(r) + sfx + " = " + R.param(rb[b]) + ";");
+                c2.s << l1.str() << d1.str();
+                for (int j = 0; j < 8; j++)
+                    c2.line("const float ra" + std::to_string(li) + "_" + std::to_string(r) + "_" + std::to_string(j) + sfx + " = " + vals[j] + ";");
+            }
+        }
+        // B runs
+        for (int r = 0; r < RUNS_B; r++) {
+            std::string rs = std::to_string(r);
+            std::string nn, kk;
+            if (contig) {
+                nn = "(n0 + (tid / 8) + " + std::to_string(r * 32) + ")";
+                kk = "(" + kt0 + " + (tid % 8) * 8)";
+            } else {
+                nn = "(n0 + (tid % " + std::to_string(BN) + "))";
+                kk = "(" + kt0 + " + ((tid / " + std::to_string(BN) + ") + " + std::to_string(r * (256 / BN)) + ") * 8)";
+            }
+            std::vector<int> rb, rd;
+            bool rok = true, rc = true;
+            std::string rr;
+            Code l1, d1;
+            l1.indent = d1.indent = c2.indent;
+            auto vals = render_weight_run(d, st.leaf[P.w], cw, {N, K}, l1, d1, nn, kk, "_b" + rs + sfx, rb, rd, rok, rc, rr);
+            for (size_t b = 0; b < rb.size(); b++)
+                c2.line("const " + std::string(ctype_of(rd[b])) + "* __restrict__ wb" + std::to_string(b) + "_b" + rs + sfx + " = " + R.param(rb[b]) + ";");
+            c2.s << l1.str();
+            if (!rr.empty()) {
+                c2.line("const sanic_u32x4 rb" + rs + sfx + " = " + rr + ";");
+            } else if (splitB) {
+                c2.s << d1.str();
+                const std::string h = "rbh" + rs + sfx, l = "rbl" + rs + sfx;
+                c2.line("unsigned " + h + "[4], " + l + "[4];");
+                for (int q = 0; q < 4; q++)
+                    c2.line("split_bf16(" + vals[2 * q] + ", " + vals[2 * q + 1] + ", " + h + "[" + std::to_string(q) + "], " + l + "[" + std::to_string(q) + "]);");
+                c2.line("const sanic_u32x4 rb" + rs + sfx + " = (sanic_u32x4){" + h + "[0], " + h + "[1], " + h + "[2], " + h + "[3]};");
+                c2.line("const sanic_u32x4 rl" + rs + sfx + " = (sanic_u32x4){" + l + "[0], " + l + "[1], " + l + "[2], " + l + "[3]};");
+            } else {
+                c2.s << d1.str();
+                c2.line("const sanic_u32x4 rb" + rs + sfx + " = (sanic_u32x4){pk_bf16(" + vals[0] + ", " + vals[1] + "), pk_bf16(" + vals[2] + ", " +
+                        vals[3] + "), pk_bf16(" + vals[4] + ", " + vals[5] + "), pk_bf16(" + vals[6] + ", " + vals[7] + ")};");
+            }
+        }
+    };
+    auto emit_stores = [&](Code& c2, const std::string& buf, const std::string& sfx) {
+        c2.line("{");
+        c2.indent++;
+        c2.line("const int ar = tid / " + std::to_string(TPR) + ";");
+        for (int r = 0; r < RUNS_A; r++) {
+            std::string rs = std::to_string(r);
+            // rest of the contraction slot (A) and the row slots, per element
+            std::string pk[4];
+            std::vector<std::string> av(8);
+            for (int j = 0; j < 8; j++) {
+                auto item = [&](int i) -> std::string {
+                    for (size_t li = 0; li < P.rows.size(); li++)
+                        if (P.rows[li] == i) return "ra" + std::to_string(li) + "_" + rs + "_" + std::to_string(j) + sfx;
+                    return "0.0f";
+                };
+                std::string v = expr_rest(R, c2, c.into[P.cslots[0]], P.w, item);
+                av[j] = v;
+                for (int sidx = 0; sidx < SR; sidx++) {
+                    std::string rv = expr_rest(R, c2, c.into[P.rslots[sidx]], -1, item);
+                    c2.line("racc" + std::to_string(sidx) + " += " + rv + ";");
+                }
+            }
+            const std::string aoff = "ar * " + std::to_string(AS) + " + (tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8);
+            if (splitA) {
+                const std::string h = R.fresh("ah"), l = R.fresh("al");
+                c2.line("unsigned " + h + "[4], " + l + "[4];");
+                for (int q = 0; q < 4; q++)
+                    c2.line("split_bf16(" + av[2 * q] + ", " + av[2 * q + 1] + ", " + h + "[" + std::to_string(q) + "], " + l + "[" + std::to_string(q) + "]);");
+                c2.line("*(sanic_u32x4*)(&a_lds[" + buf + "][" + aoff + "]) = (sanic_u32x4){" + h + "[0], " + h + "[1], " + h + "[2], " + h + "[3]};");
+                c2.line("*(sanic_u32x4*)(&a_lo[" + buf + "][" + aoff + "]) = (sanic_u32x4){" + l + "[0], " + l + "[1], " + l + "[2], " + l + "[3]};");
+            } else {
+                c2.line("*(sanic_u32x4*)(&a_lds[" + buf + "][" + aoff + "]) = (sanic_u32x4){pk_bf16(" + av[0] + ", " + av[1] + "), pk_bf16(" + av[2] + ", " + av[3] +
+                        "), pk_bf16(" + av[4] + ", " + av[5] + "), pk_bf16(" + av[6] + ", " + av[7] + ")};");
+            }
+        }
+        for (int r = 0; r < RUNS_B; r++) {
+            std::string rs = std::to_string(r);
+            std::string row, col;
+            if (contig) {
+                row = "((tid / 8) + " + std::to_string(r * 32) + ")";
+                col = "((tid % 8) * 8)";
+            } else {
+                row = "(tid % " + std::to_string(BN) + ")";
+                col = "(((tid / " + std::to_string(BN) + ") + " + std::to_string(r * (256 / BN)) + ") * 8)";
+            }
+            c2.line("*(sanic_u32x4*)(&b_lds[" + buf + "][" + row + " * " + std::to_string(BS) + " + " + col + "]) = rb" + rs + sfx + ";");
+            if (splitB) c2.line("*(sanic_u32x4*)(&b_lo[" + buf + "][" + row + " * " + std::to_string(BS) + " + " + col + "]) = rl" + rs + sfx + ";");
+        }
+        c2.indent--;
+        c2.line("}");
+    };
+    auto emit_mfma = [&](Code& c2, const std::string& buf) {
+        c2.line("#pragma unroll");
+        c2.line("for (int ks = 0; ks < 2; ++ks) {");
+        const std::string MTs = std::to_string(MT), NTs = std::to_string(NT);
+        const std::string aidx = "[(wm + i * 16 + l16) * " + std::to_string(AS) + " + ks * 32 + lq * 8]";
+        const std::string bidx = "[(wn + j * 16 + l16) * " + std::to_string(BS) + " + ks * 32 + lq * 8]";
+        c2.line("  bf16x8 af[" + MTs + "], bf[" + NTs + "];");
+        if (splitA) c2.line("  bf16x8 afl[" + MTs + "];");
+        if (splitB) c2.line("  bf16x8 bfl[" + NTs + "];");
+        c2.line("  #pragma unroll");
+        c2.line("  for (int i = 0; i < " + MTs + "; ++i) {");
+        c2.line("    af[i] = *(const bf16x8*)(&a_lds[" + buf + "]" + aidx + ");");
+        if (splitA) c2.line("    afl[i] = *(const bf16x8*)(&a_lo[" + buf + "]" + aidx + ");");
+        c2.line("  }");
+        c2.line("  #pragma unroll");
+        c2.line("  for (int j = 0; j < " + NTs + "; ++j) {");
+        c2.line("    bf[j] = *(const bf16x8*)(&b_lds[" + buf + "]" + bidx + ");");
+        if (splitB) c2.line("    bfl[j] = *(const bf16x8*)(&b_lo[" + buf + "]" + bidx + ");");
+        c2.line("  }");
+        c2.line("  #pragma unroll");
+        c2.line("  for (int i = 0; i < " + MTs + "; ++i)");
+        c2.line("    #pragma unroll");
+        c2.line("    for (int j = 0; j < " + NTs + "; ++j) {");
+        c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);");
+        if (splitA) c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afl[i], bf[j], acc[i][j], 0, 0, 0);");
+        if (splitB) c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfl[j], acc[i][j], 0, 0, 0);");
+        c2.line("    }");
+        c2.line("}");
+    };
+    const int64_t NKT = K / 64;
+    k.line("{");
+    k.indent++;
+    emit_loads(k, "(idx_t)0", "_0");
+    emit_stores(k, "0", "_0");
+    k.indent--;
+    k.line("}");
+    k.line("__syncthreads();");
+    k.line("for (idx_t kt = 0; kt < " + std::to_string(NKT) + "; ++kt) {");
+    k.indent++;
+    k.line("const int buf = (int)(kt & 1);");
+    k.line("const bool more = kt + 1 < " + std::to_string(NKT) + ";");
+    // next tile's loads in flight during this tile's MFMAs (the last step re-reads tile 0)
+    emit_loads(k, "(((kt + 1) % " + std::to_string(NKT) + ") * 64)", "_n");
+    emit_mfma(k, "buf");
+    k.line("if (more) {");
+    k.indent++;
+    emit_stores(k, "buf ^ 1", "_n");
+    k.indent--;
+    k.line("}");
+    k.line("__syncthreads();");
+    k.indent--;
+    k.line("}");
+    // row slots: sum the TPR partial rows, publish per row
+    if (SR) {
+        for (int i = 0; i < SR; i++) {
+            std::string r = "racc" + std::to_string(i);
+            for (int off = 1; off < TPR; off <<= 1) k.line(r + " += __shfl_xor(" + r + ", " + std::to_string(off) + ", 64);");
+            k.line("if (tid % " + std::to_string(TPR) + " == 0) rs_lds[(tid / " + std::to_string(TPR) + ") * " + std::to_string(SR) + " + " + std::to_string(i) + "] = " + r + ";");
+        }
+        k.line("__syncthreads();");
+    }
+    // finish: project, epilogue, narrowing store per element
+    k.line("#pragma unroll");
+    k.line("for (int i = 0; i < " + std::to_string(MT) + "; ++i)");
+    k.line("  #pragma unroll");
+    k.line("  for (int j = 0; j < " + std::to_string(NT) + "; ++j)");
+    k.line("    #pragma unroll");
+    k.line("    for (int r = 0; r < 4; ++r) {");
+    k.indent += 3;
+    k.line("const int ml = wm + i * 16 + lq * 4 + r;");
+    k.line("const idx_t gm = m0 + ml, gn = n0 + wn + j * 16 + l16;");
+    k.line("const float fs" + std::to_string(P.cslots[0]) + " = acc[i][j][r];");
+    for (int i = 0; i < SR; i++)
+        k.line("const float fs" + std::to_string(P.rslots[i]) + " = rs_lds[ml * " + std::to_string(SR) + " + " + std::to_string(i) + "];");
+    R.memo.emplace_back();
+    std::string f = R.expr(k, c.project, "", "", "", "fs");
+    k.line("const float fold_v = " + f + ";");
+    std::vector<std::string> gc(st.rank, "0");
+    gc[P.mdim] = "gm";
+    gc[P.ndim] = "gn";
+    std::string v = "fold_v";
+    if (st.epilogue >= 0) {
+        R.fold_var = "fold_v";
+        v = R.value(k, st.epilogue, gc);
+    }
+    R.memo.pop_back();
+    std::string lin;
+    for (int j = 0; j < st.rank; j++)
+        lin = j == 0 ? "(idx_t)(" + gc[0] + ")" : "(" + lin + " * " + std::to_string(st.grid[j]) + " + (idx_t)(" + gc[j] + "))";
+    k.line(store_stmt(R.param(st.out_buffer), lin, st.out_dtype, v));
+    k.indent -= 3;
+    k.line("    }");
+
+    const std::string kname = "sanic_gemm_" + std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K);
+    std::ostringstream src;
+    src << kPrelude;
+    src << "typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;\n";
+    src << "typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;\n";
+    src << "typedef __bf16 sanic_bf16x2 __attribute__((ext_vector_type(2)));\n";
+    src << "typedef float sanic_f32x2 __attribute__((ext_vector_type(2)));\n";
+    src << "__device__ __forceinline__ unsigned pk_bf16(float x, float y) {\n"
+           "  return __builtin_bit_cast(unsigned, __builtin_convertvector((sanic_f32x2){x, y}, sanic_bf16x2));\n}\n";
+    src << "__device__ __forceinline__ void split_bf16(float x, float y, unsigned& hi, unsigned& lo) {\n"
+           "  const unsigned h = pk_bf16(x, y);\n"
+           "  hi = h;\n"
+           "  lo = pk_bf16(x - __uint_as_float(h << 16), y - __uint_as_float(h & 0xFFFF0000u));\n}\n";
+    src << R.args_struct({});
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
+    out.kernel_kind = "skeleton:gemm[" + std::to_string(BM) + "x" + std::to_string(BN) + (splitA ? ",a2" : "") + (splitB ? ",b2" : "") + "]";
+    out.source = src.str();
+    out.launches.push_back({kname, "", dim3((unsigned)((M / BM) * (N / BN))), dim3(256), 0, R.arg_list()});
+    return true;
+}
+
+}  // namespace sanic

@@ -215,6 +215,7 @@ struct VecW {
     bool ok = true;
     bool contiguous = true;       // every access moves by 0 or 1 element along k
     std::string nn = "nn", k0 = "k0", ptr = "wb", psfx, sfx;
+    std::string last_raw;     // the 128-bit bf16 register of the last contiguous access
     std::string fresh(const char* p) { return std::string(p) + std::to_string(tmp++) + sfx; }
 
     std::vector<std::string> render(Code& lc, Code& dc, int node, const std::vector<Sym>& c, const std::vector<int64_t>& ext) {
@@ -280,6 +281,7 @@ struct VecW {
         if (jstride == 1 && acc.dtype == SANIC_BF16) {
             std::string v = fresh("wq");
             lc.line("const sanic_u32x4 " + v + " = __builtin_nontemporal_load((const sanic_u32x4*)(" + p + " + " + base + "));");
+            last_raw = v;
             for (int j = 0; j < 8; j++)
                 out[j] = std::string("__uint_as_float(") + (j % 2 == 0 ? "(" + v + "." + comp[j / 2] + " << 16)"
                                                                         : "(" + v + "." + comp[j / 2] + " & 0xFFFF0000u)") + ")";
@@ -309,6 +311,28 @@ struct VecW {
         return out;
     }
 };
+
+// One run of 8 of a leaf at (nn, k0) through the vector renderer (used by the GEMM skeleton).
+// `raw_bf16` names the 128-bit register when the leaf is exactly one contiguous bf16 access.
+std::vector<std::string> render_weight_run(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
+                                           const std::vector<int64_t>& ext, Code& lc, Code& dc, const std::string& nn,
+                                           const std::string& k0, const std::string& sfx, std::vector<int>& bufs,
+                                           std::vector<int>& dtypes, bool& ok, bool& contiguous, std::string& raw_bf16) {
+    VecW vw{d};
+    vw.nn = nn;
+    vw.k0 = k0;
+    vw.ptr = "wb";
+    vw.psfx = sfx;
+    vw.sfx = sfx;
+    auto vals = vw.render(lc, dc, node, c, ext);
+    bufs = vw.bufs;
+    dtypes = vw.dtypes;
+    ok = vw.ok;
+    contiguous = vw.contiguous;
+    int kind = d->nodes[node].kind;
+    raw_bf16 = (bufs.size() == 1 && dtypes[0] == SANIC_BF16 && kind != SANIC_NODE_MAP && kind != SANIC_NODE_CONST) ? vw.last_raw : "";
+    return vals;
+}
 
 // ───────────────────────── gemv ───────────────────────────────────────────────────────────
 
@@ -825,6 +849,7 @@ bool lower_pointwise_skeleton(const sanic_program_desc* d, int si, int64_t&, Low
 }
 
 bool lower_skeleton(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
+    if (lower_gemm(d, si, scratch, out)) return true;
     if (lower_flash_prefill(d, si, scratch, out)) return true;
     if (lower_attn_decode(d, si, scratch, out)) return true;
     return false;

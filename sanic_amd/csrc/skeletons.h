@@ -38,6 +38,7 @@ bool sym_access(const sanic_program_desc* d, int node, const std::vector<Sym>& c
 bool sym_child_coords(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
                       const std::vector<int64_t>& ext, std::vector<Sym>& sc);
 
+bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out);
 bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out);
 bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out);
 

@@ -1,0 +1,57 @@
+"""MFMA GEMM skeleton (configs B2 and D2, plus small ragged shapes) against the oracle."""
+import numpy as np
+import pytest
+
+import oracle
+from sanic_amd import configs, ir
+from sanic_amd.backend import from_bf16_bits
+from tests.test_gpu_skeletons import bf16_rel, _bf16_vals
+from tests.util import run_on_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _report(exe, got, want):
+    got = np.asarray(got, np.float64).reshape(want.shape)
+    rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-3)
+    bad = np.argwhere(rel > 2e-2)
+    print(exe.stage_kernel(0), float(rel.max()), "bad", len(bad), bad[:8].tolist(), flush=True)
+
+
+@pytest.mark.parametrize("M,K,N,kmajor", [
+    (512, 2048, 8192, True),      # config B2, W [K, N]
+    (512, 2048, 8192, False),     # same with the reference's [out, in] layout
+    (64, 256, 96, True),
+    (192, 128, 160, False),
+])
+def test_rmsnorm_gemm(dev, M, K, N, kmajor):
+    prog = configs.rmsnorm_projection(M=M, K=K, N=N, kmajor=kmajor)
+    x = _bf16_vals(301, M * K).reshape(M, K)
+    g = _bf16_vals(302, K, 1.0, 0.02)
+    wbits = oracle.synth_bf16(303, N * K, "normal", 0.0, 0.02)
+    wkn = wbits.reshape(K, N) if kmajor else np.ascontiguousarray(wbits.reshape(N, K).T)
+    w = from_bf16_bits(wbits).astype(np.float64).reshape((K, N) if kmajor else (N, K))
+    got, exe = run_on_gpu(dev, prog, {"x": x, "g": g, "W": w})
+    want = oracle.rmsnorm_proj(x, g, np.ascontiguousarray(wkn), 1e-5)
+    err = bf16_rel(got["y"], want)
+    _report(exe, got["y"], want)
+    assert exe.stage_kernel(0).startswith("skeleton:gemm")
+    assert err < 2e-2
+
+
+@pytest.mark.parametrize("M,K,N,G", [(128, 2048, 8192, 64), (64, 512, 256, 32)])
+def test_int4_gemm(dev, M, K, N, G):
+    """Config D2: packed uint4 [N, K], per-group scale and zero point, w = u·s − z."""
+    prog = configs.int4_matmul(M=M, K=K, N=N, G=G)
+    rng = np.random.default_rng(11)
+    u = rng.integers(0, 16, size=(N, K))
+    s = _bf16_vals(401, N * K // G, 0.001, 0.02, kind="uniform").reshape(N, K // G)
+    z = np.array([oracle.round_bf16(8.0 * v) for v in s.reshape(-1)]).reshape(s.shape)
+    x = _bf16_vals(402, M * K).reshape(M, K)
+    got, exe = run_on_gpu(dev, prog, {"x": x, "Wq": u.reshape(N, K // G, G), "S": s, "Z": z})
+    packed = (u[:, 0::2] | (u[:, 1::2] << 4)).astype(np.uint8)
+    want = oracle.int4_matmul(x, packed, s, z, G)
+    err = bf16_rel(got["y"], want)
+    _report(exe, got["y"], want)
+    assert exe.stage_kernel(0).startswith("skeleton:gemm")
+    assert err < 2e-2
