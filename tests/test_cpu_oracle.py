@@ -329,3 +329,56 @@ def test_reserved_cache_length_does_not_change_decode():
     a = oracle.run_program(prog_s, {"q": q, "k_cache": k, "v_cache": v, "position": np.array(5.0)})["o"]
     b = oracle.run_program(prog_l, {"q": q, "k_cache": kl, "v_cache": vl, "position": np.array(5.0)})["o"]
     np.testing.assert_allclose(a, b, rtol=1e-12)
+
+
+def _numpy_attention(q, k, v, scale, visible):
+    """Brute-force softmax attention with an explicit visibility matrix (GQA by h // rep)."""
+    Hq, Hkv = q.shape[0], k.shape[0]
+    rep = Hq // Hkv
+    out = np.empty((Hq, q.shape[1], v.shape[2]))
+    for h in range(Hq):
+        s = q[h] @ k[h // rep].T * scale
+        s = np.where(visible, s, -np.inf)
+        e = np.exp(s - s.max(-1, keepdims=True))
+        out[h] = (e / e.sum(-1, keepdims=True)) @ v[h // rep]
+    return out
+
+
+@pytest.mark.parametrize("window", [0, 1, 5])
+def test_fused_attention_masks_against_brute_force(window):
+    """oracle.attention's causal (mask 1), sliding-window (mask 2: q − W + 1 ≤ k ≤ q) and
+    decode prefix (mask 3: k ≤ q_pos0 for every query row) masks, with GQA, against an explicit mask matrix."""
+    Hq, Hkv, S, D = 4, 2, 9, 8
+    q = oracle.lcg(41, Hq * S * D).reshape(Hq, S, D)
+    k = oracle.lcg(42, Hkv * S * D).reshape(Hkv, S, D)
+    v = oracle.lcg(43, Hkv * S * D).reshape(Hkv, S, D)
+    qi, ki = np.arange(S)[:, None], np.arange(S)[None, :]
+    if window:
+        vis = (ki <= qi) & (ki >= qi - window + 1)
+        got = oracle.attention(q, k, v, 0.3, mask=2, window=window)
+    else:
+        vis = ki <= qi
+        got = oracle.attention(q, k, v, 0.3, mask=1)
+    np.testing.assert_allclose(got, _numpy_attention(q, k, v, 0.3, vis), rtol=1e-12, atol=1e-14)
+    pre = oracle.attention(q[:, 2:4], k, v, 0.3, mask=3, q_pos0=4)
+    np.testing.assert_allclose(pre, _numpy_attention(q[:, 2:4], k, v, 0.3, np.broadcast_to(ki <= 4, (2, S))),
+                               rtol=1e-12, atol=1e-14)
+
+
+@pytest.mark.parametrize("window", [0, 3])
+def test_flash_prefill_graph_equals_fused_attention(window):
+    """The config-C graph (RoPE stages, GQA expand, causal and window masks as additive where
+    terms) under the interpreter equals the fused attention over RoPE'd inputs."""
+    NH, NKV, S, HD = 4, 2, 8, 8
+    prog = configs.flash_prefill(NH, NKV, S, HD, theta=10000.0, window=window)
+    vals = {"Q": oracle.lcg(51, NH * S * HD).reshape(NH, S, HD),
+            "K": oracle.lcg(52, NKV * S * HD).reshape(NKV, S, HD),
+            "V": oracle.lcg(53, NKV * S * HD).reshape(NKV, S, HD)}
+    rb = np.vectorize(oracle.round_bf16)
+    vals = {n: rb(a) for n, a in vals.items()}
+    got = oracle.run_program(prog, vals)
+    invf = oracle.inv_freq(10000.0, HD // 2)
+    qr, kr = rb(oracle.rope(vals["Q"], 0, invf)), rb(oracle.rope(vals["K"], 0, invf))
+    np.testing.assert_allclose(got["Qr"], qr, rtol=0, atol=0)
+    want = oracle.attention(qr, kr, vals["V"], 1 / np.sqrt(HD), mask=2 if window else 1, window=window)
+    np.testing.assert_allclose(got["O"], rb(want), rtol=2 ** -7, atol=1e-6)
