@@ -73,7 +73,7 @@ def dominant_kernel_roofline(dev, shape, weights, reps=50):
     nbytes = 2 * F * H * 2 + H * 4 + H * 2 + 2 * F * 4
     kname = exe.stage_kernel(0)
     return {"bound": "hbm", "achieved": nbytes / secs / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": nbytes / secs / HBM_PEAK, "traffic": None,
+            "frac": nbytes / secs / HBM_PEAK, "traffic": traffic_from_profile(),
             "kernel": f"sanic_gemv_{2 * F}x{H} ({kname})", "bytes_per_launch": nbytes,
             "us_per_launch": secs * 1e6}
 
@@ -222,14 +222,61 @@ def bench_config(name: str, copies: int = 8):
     print(json.dumps(out), flush=True)
 
 
+def pmc_probe(reps=20):
+    """A short program for the rocprofv3 --pmc passes: `reps` launches of the dominant kernel
+    (the batched gate/up GEMV, layer-0 shapes) and `reps` plain device copies of 256 MiB, whose
+    known byte counts calibrate FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    from sanic_amd import configs
+    from sanic_amd.backend import HipDevice
+    torch.cuda.init()
+    dev = HipDevice(0)
+    shape = configs.LlamaShape(layers=1)
+    H, F = shape.hidden, shape.ffn
+    keep, weights = [], {}
+    pre = "model.layers.0."
+    for nm, shp in ((pre + "post_attention_layernorm.weight", (H,)), (pre + "mlp.gate_proj.weight", (F, H)),
+                    (pre + "mlp.up_proj.weight", (F, H))):
+        t = (torch.randn(shp, device="cuda") * 0.02).to(torch.bfloat16)
+        keep.append(t)
+        weights[nm] = dev.wrap(t.data_ptr(), t.numel() * 2)
+    torch.cuda.synchronize()
+    roof = dominant_kernel_roofline(dev, shape, weights, reps=reps)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": roof["kernel"], "us_per_launch": roof["us_per_launch"],
+                      "copy_bytes": 256 << 20}), flush=True)
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the dominant kernel from the committed PMC summary (the
+    `traffic_bytes_per_launch:` line written from two rocprofv3 --pmc passes), or None."""
+    path = os.path.join(ROOT, "profiles", "gateup_gemv_16384x2048_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true", help="run only the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--config", default=None, help="measure a secondary configuration instead: " + ", ".join(CONFIGS))
     args = ap.parse_args()
+    if args.pmc_probe:
+        pmc_probe()
+        return
     if args.config:
         import torch
         torch.cuda.init()
