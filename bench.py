@@ -48,9 +48,11 @@ def device_weights(dev, shape, seed=1234):
     return bufs, keep
 
 
-def dominant_kernel_roofline(dev, shape, weights, reps=50):
-    """Replay the gate/up norm-fused GEMV (one launch, N = 2·ffn, K = hidden) back to back in a
-    hipGraph and time it with HIP events on the library's stream."""
+def dominant_kernel_roofline(dev, shape, weights, reps=40, copies=8):
+    """The decode step's dominant kernel — the batched gate/up RMSNorm-fused GEMV with the
+    SwiGLU product computed per row pair (one launch: N = 2·ffn rows, K = hidden), on layer 0's
+    weights — `copies` launches per hipGraph replay, timed with HIP events on the library's
+    stream over `reps` back-to-back replays. Per-launch time = total / (reps · copies)."""
     from sanic_amd import carrier as C
     from sanic_amd import ir
     from sanic_amd.program import STREAM, Program
@@ -58,47 +60,27 @@ def dominant_kernel_roofline(dev, shape, weights, reps=50):
     p = Program()
     x = p.input("x", (H,), ir.F32)
     g = p.input("g", (H,), ir.BF16)
-    for nm in ("gate", "up"):
-        w = p.input(f"W{nm}", (F, H), ir.BF16)
-        p.fused(nm, (F,), H, [(x, (STREAM,)), (g, (STREAM,)), (w, (0, STREAM))],
-                C.norm_fused_projection(H, shape.eps), ir.F32)
+    ws = {nm: p.input(f"W{nm}", (F, H), ir.BF16) for nm in ("gate", "up")}
+    for r in range(copies):
+        gu = {nm: p.fused(f"{nm}{r}", (F,), H, [(x, (STREAM,)), (g, (STREAM,)), (ws[nm], (0, STREAM))],
+                          C.norm_fused_projection(H, shape.eps), ir.F32) for nm in ("gate", "up")}
+        p.pointwise(f"h{r}", ir.map_(ir.MUL, ir.silu(gu["gate"]), gu["up"]), ir.F32)
     exe = dev.prepare(p)
+    kname = exe.stage_kernel(0)
+    assert kname.startswith("skeleton:gemv[batched 2]+paired"), kname
     xb = dev.from_values([0.5] * H, ir.F32)
     pre = "model.layers.0."
     binds = {"x": xb, "g": weights[pre + "post_attention_layernorm.weight"],
              "Wgate": weights[pre + "mlp.gate_proj.weight"], "Wup": weights[pre + "mlp.up_proj.weight"]}
     rp = exe.capture(binds)
     rp.step_many(5)
-    secs = rp.step_many(reps) / reps
-    nbytes = 2 * F * H * 2 + H * 4 + H * 2 + 2 * F * 4
-    kname = exe.stage_kernel(0)
+    secs = rp.step_many(reps) / (reps * copies)
+    # weights + x (f32) + gain (bf16) + gate, up and h outputs (f32)
+    nbytes = 2 * F * H * 2 + H * 4 + H * 2 + 3 * F * 4
     return {"bound": "hbm", "achieved": nbytes / secs / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": nbytes / secs / HBM_PEAK, "traffic": traffic_from_profile(),
             "kernel": f"sanic_gemv_{2 * F}x{H} ({kname})", "bytes_per_launch": nbytes,
             "us_per_launch": secs * 1e6}
-
-
-def cpu_baseline(shape, seconds_budget=20.0):
-    """The oracle's fused f64 decode step (oracle_llama_step) on this host at position 2048."""
-    import ctypes
-    import numpy as np
-    import oracle
-    from tests.llama_ref import OracleModel, synth_weights
-    threads = oracle.threads()
-    w = synth_weights(shape, seed=99)
-    om = OracleModel(shape, w)
-    n, t0 = 0, time.perf_counter()
-    tok = 1
-    while True:
-        tok, _ = om.step(tok, PROMPT + n)
-        n += 1
-        el = time.perf_counter() - t0
-        if el > seconds_budget / 4 or n >= 8:
-            break
-    return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps of the full model at positions {PROMPT}..{PROMPT + n - 1} "
-                      f"(f64 fused loops over bf16 weights, {threads} threads, "
-                      f"{os.uname().nodename})"}
 
 
 # ── secondary configurations (BASELINE.json configs B, C, D): one dominant kernel each ──

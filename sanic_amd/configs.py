@@ -152,7 +152,7 @@ def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
       folds (norm-fused carrier) → in-place K/V cache row writes (update_cache, RoPE on k) →
       decode attention over the cache (online-softmax carrier; RoPE on q inside its leaf, the
       −∞ prefix mask of positions > pos) → o projection + residual (epilogue) → gate/up with
-      the post-attention RMSNorm fused → down projection over silu(gate)·up (a leaf) +
+      the post-attention RMSNorm fused → silu(gate)·up (elementwise) → down projection +
       residual → final RMSNorm fused into the tied lm_head → argmax (key/tie carrier).
     Intermediates are stored f32; weights and the K/V caches are bf16; `token` is u32."""
     S = shape
@@ -214,7 +214,9 @@ def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
             w = p.node(pre + f"mlp.{nm}_proj.weight")
             gu[nm] = p.fused(f"{pre}{nm}", (F,), H, [(x, (STREAM,)), (g2, (STREAM,)), (w, (0, STREAM))],
                              C.norm_fused_projection(H, S.eps), ir.F32, role=3)
-        hsw = ir.map_(ir.MUL, ir.silu(gu["gate"]), gu["up"])
+        # the SwiGLU cone as its own elementwise stage (a cut the partitioner makes so the
+        # down projection's leaf is a plain load, not silu recomputed per output row)
+        hsw = p.pointwise(f"{pre}mlp.h", ir.map_(ir.MUL, ir.silu(gu["gate"]), gu["up"]), ir.F32, role=3)
         wd = p.node(pre + "mlp.down_proj.weight")
         x = p.fused(f"{pre}x_mlp", (H,), F, [(hsw, (STREAM,)), (wd, (0, STREAM))], C.dot(2), ir.F32,
                     epilogue=ir.map_(ir.ADD, x, ir.fold_value((H,))), role=3)

@@ -300,10 +300,12 @@ std::string map_expr(int op, const std::string& a, const std::string& b, const s
     case SANIC_OP_MIN: return "fminf(" + a + ", " + b + ")";
     case SANIC_OP_LT: return "((" + a + " < " + b + ") ? 1.0f : 0.0f)";
     case SANIC_OP_NEG: return "(-" + a + ")";
-    case SANIC_OP_RECIP: return "(1.0f / " + a + ")";
-    case SANIC_OP_EXP: return "expf(" + a + ")";
-    case SANIC_OP_LOG: return "logf(" + a + ")";
-    case SANIC_OP_SQRT: return "sqrtf(" + a + ")";
+    // relaxed math, as the reference compiles its kernels (metal.rs:164-172): the hardware
+    // exp2 / log2 / reciprocal / square root (about 1 ulp) instead of the libm sequences
+    case SANIC_OP_RECIP: return "__builtin_amdgcn_rcpf(" + a + ")";
+    case SANIC_OP_EXP: return "__builtin_amdgcn_exp2f((" + a + ") * 1.44269504088896341f)";
+    case SANIC_OP_LOG: return "(__builtin_amdgcn_logf(" + a + ") * 0.693147180559945309f)";
+    case SANIC_OP_SQRT: return "__builtin_amdgcn_sqrtf(" + a + ")";
     case SANIC_OP_TANH: return "tanhf(" + a + ")";
     case SANIC_OP_SIN: return "sinf(" + a + ")";
     case SANIC_OP_COS: return "cosf(" + a + ")";
@@ -1055,6 +1057,13 @@ Lowered lower_program(const sanic_program_desc* d) {
             s += (int)tails.size();
         } else {
             LoweredStage L;
+            int ab = getenv("SANIC_HIP_GENERIC") ? -1 : attn_absorber(d, s);
+            if (ab >= 0) {
+                L.kernel_kind = "absorbed-into:" + std::to_string(ab);
+                out.stages.push_back(std::move(L));
+                s++;
+                continue;
+            }
             if (getenv("SANIC_HIP_GENERIC") || !lower_pointwise_skeleton(d, s, out.scratch_bytes, L))
                 L = lower_pointwise(d, s);
             out.stages.push_back(std::move(L));

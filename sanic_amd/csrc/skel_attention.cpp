@@ -228,7 +228,92 @@ bool attn_plan(const sanic_program_desc* d, int si, AttnPlan& P) {
     return true;
 }
 
+// ── in-place K/V row writes performed by the attention kernel ──
+// The decode step writes this position's K row and V column into the caches (a pointwise stage
+// with a row `where`, emit_metal.rs:1103-1178) right before the attention reads them. The
+// attention kernel does those writes itself: the workgroup whose chunk holds the row computes
+// the group's row elements, stores them, and uses the stored (narrowed) values in place of the
+// ones it prefetched, so no other launch or cross-workgroup ordering is needed.
+struct RowWrite {
+    int stage = -1, buffer = -1, rdim = -1, pos = -1;
+    bool is_k = false;
+    std::vector<int64_t> shape, stride;
+};
+
+int64_t eval_sym(const Sym& s, const std::vector<int64_t>& v) {
+    int64_t r = s.c0;
+    for (auto& t : s.terms) {
+        int64_t x = v[t.var] / t.div;
+        if (t.mod) x %= t.mod;
+        r += t.coef * x;
+    }
+    return r;
+}
+
+// Does the attention's read of `acc` over (grp, t, x) (x < X) touch exactly the row t of the
+// buffer, every element of it once across all groups?
+bool row_mapping_ok(const Sym& addr, int REP, int64_t NG, int64_t T, int64_t X, const RowWrite& w) {
+    int64_t vol = 1;
+    for (auto e : w.shape) vol *= e;
+    if (w.shape[w.rdim] != T || vol / T != NG * X) return false;
+    for (int64_t t : {(int64_t)0, T / 2, T - 1}) {
+        std::set<int64_t> seen;
+        for (int64_t g = 0; g < NG; g++)
+            for (int64_t x = 0; x < X; x++) {
+                int64_t f = eval_sym(addr, {g * REP, t, x});
+                if (f < 0 || f >= vol || (f / w.stride[w.rdim]) % w.shape[w.rdim] != t) return false;
+                seen.insert(f);
+            }
+        if ((int64_t)seen.size() != NG * X) return false;
+    }
+    return true;
+}
+
+std::vector<RowWrite> absorbed_writes(const sanic_program_desc* d, int ai, const AttnPlan& P) {
+    std::vector<RowWrite> out;
+    if (getenv("SANIC_HIP_NO_ABSORB") || getenv("SANIC_HIP_GENERIC")) return out;
+    const int64_t NG = P.NH / P.rep;
+    for (int s = ai - 1; s >= 0 && out.size() < 2; s--) {
+        const sanic_stage& st = d->stages[s];
+        if (st.kind != SANIC_STAGE_POINTWISE || st.where < 0) break;
+        RowWrite w;
+        w.stage = s;
+        w.buffer = st.out_buffer;
+        if (d->buffers[w.buffer].role != SANIC_BUF_STATE) break;
+        if (!match_row_cond(d, st.where, st.rank, w.rdim, w.pos)) break;
+        if (w.buffer == P.dot.kacc.buffer) w.is_k = true;
+        else if (w.buffer != P.vacc.buffer) break;
+        bool dup = false;
+        for (auto& o : out) dup |= o.buffer == w.buffer;
+        if (dup) break;
+        std::set<int> reads;
+        collect_inputs(d, st.value, reads);
+        collect_inputs(d, st.where, reads);
+        if (reads.count(P.dot.kacc.buffer) || reads.count(P.vacc.buffer)) break;
+        for (int j = 0; j < st.rank; j++) w.shape.push_back(st.grid[j]);
+        w.stride.assign(st.rank, 1);
+        for (int j = st.rank - 2; j >= 0; j--) w.stride[j] = w.stride[j + 1] * w.shape[j + 1];
+        bool ok = w.is_k ? row_mapping_ok(P.dot.kacc.addr, P.rep, NG, P.T, P.dot.depth, w)
+                         : row_mapping_ok(P.vacc.addr, P.rep, NG, P.T, P.E, w);
+        if (!ok) break;
+        out.push_back(w);
+    }
+    return out;
+}
+
 }  // namespace
+
+int attn_absorber(const sanic_program_desc* d, int si) {
+    if (si >= d->n_stages || d->stages[si].kind != SANIC_STAGE_POINTWISE) return -1;
+    int ai = si + 1;
+    while (ai < d->n_stages && d->stages[ai].kind == SANIC_STAGE_POINTWISE && d->stages[ai].where >= 0) ai++;
+    if (ai >= d->n_stages || ai - si > 2) return -1;
+    AttnPlan P;
+    if (!attn_plan(d, ai, P)) return -1;
+    for (auto& w : absorbed_writes(d, ai, P))
+        if (w.stage == si) return ai;
+    return -1;
+}
 
 bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
     AttnPlan P;
@@ -246,10 +331,16 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     int64_t part_off = scratch;
     scratch += ((NCH * NH * PSZ * 4 + 255) / 256) * 256;
 
+    const std::vector<RowWrite> writes = absorbed_writes(d, si, P);
+    bool wk = false, wvv = false;
+    for (auto& w : writes) (w.is_k ? wk : wvv) = true;
+    if (wvv && !(P.vacc.dtype == SANIC_BF16)) return false;
     Renderer R(d);
     Code k;
     k.indent = 1;
     k.line("__shared__ float q_lds[" + std::to_string(REP * HD) + "];");
+    if (wk) k.line("__shared__ float knew_lds[" + std::to_string(HD) + "];");
+    if (wvv) k.line("__shared__ float vnew_lds[" + std::to_string(E) + "];");
     k.line("__shared__ float p_lds[" + std::to_string(REP) + "][" + std::to_string(CH) + "];");
     k.line("__shared__ float stat_lds[" + std::to_string(REP) + "][2];");
     k.line("__shared__ float o_lds[4][" + std::to_string(REP) + "][" + std::to_string(E) + "];");
@@ -317,6 +408,49 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("  vq[sb][1] = *(const sanic_u32x4*)(src + 8);");
         k.line("}");
     }
+    // absorbed row writes: the workgroup whose chunk holds the row (chunk 0 when the row is
+    // outside the window) computes and stores this group's row elements
+    for (auto& w : writes) {
+        const sanic_stage& wst = d->stages[w.stage];
+        const std::string nm = w.is_k ? "k" : "v";
+        const int64_t X = w.is_k ? HD : E;
+        const Sym& addr = w.is_k ? P.dot.kacc.addr : P.vacc.addr;
+        R.memo.emplace_back();
+        const sanic_node& pn = d->nodes[w.pos];
+        std::string pv = R.value(k, w.pos, std::vector<std::string>(pn.rank, "0"));
+        R.memo.pop_back();
+        k.line("const float " + nm + "pf = roundf(" + pv + ");");
+        k.line("const idx_t " + nm + "row = (" + nm + "pf >= 0.0f && " + nm + "pf < " + std::to_string(T) + ".0f) ? (idx_t)" + nm + "pf : -1;");
+        k.line("const bool " + nm + "writer = " + nm + "row >= 0 && chunk == ((" + nm + "row >= lo0 && " + nm + "row < hi0) ? (" + nm + "row - lo0) / " +
+               std::to_string(CH) + " : 0);");
+        k.line("if (" + nm + "writer) {");
+        k.indent++;
+        k.line("for (int xw = tid; xw < " + std::to_string(X) + "; xw += 256) {");
+        k.indent++;
+        k.line("const idx_t wf = " + addr.render({"(grp * " + std::to_string(REP) + ")", nm + "row", "xw"}) + ";");
+        std::vector<std::string> wc;
+        for (size_t j = 0; j < w.shape.size(); j++) {
+            k.line("const idx_t w" + nm + std::to_string(j) + " = (wf / " + std::to_string(w.stride[j]) + ") % " + std::to_string(w.shape[j]) + ";");
+            wc.push_back("w" + nm + std::to_string(j));
+        }
+        R.memo.emplace_back();
+        std::string cond = R.value(k, wst.where, wc);
+        std::string val = R.value(k, wst.value, wc);
+        R.memo.pop_back();
+        k.line("float " + nm + "val = " + val + ";");
+        k.line("if (" + cond + " != 0.0f) {");
+        k.line("  " + store_stmt(R.param(w.buffer), "wf", d->buffers[w.buffer].dtype, nm + "val"));
+        if (d->buffers[w.buffer].dtype == SANIC_BF16) k.line("  " + nm + "val = __uint_as_float((unsigned)sanic_to_bf16(" + nm + "val) << 16);");
+        k.line("} else {");
+        k.line("  " + nm + "val = " + (w.is_k ? std::string("sanic_bf16(kp[") + nm + "row * " + std::to_string(kt) + " + xw])"
+                                                  : std::string("sanic_bf16(vp[xw * ") + std::to_string(ve) + " + " + nm + "row * " + std::to_string(vt) + "])") + ";");
+        k.line("}");
+        k.line(nm + "new_lds[xw] = " + nm + "val;");
+        k.indent--;
+        k.line("}");
+        k.indent--;
+        k.line("}");
+    }
     // query vectors (the A side, rendered) into LDS, after the K/V prefetch is issued: its latency hides behind the q-side arithmetic
     if (REP * HD == 256) k.line("{ const int i = tid;");
     else k.line("for (int i = tid; i < " + std::to_string(REP * HD) + "; i += 256) {");
@@ -346,7 +480,13 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.indent++;
     k.line("const int d0 = sub * " + std::to_string(DPL) + " + v8 * 8;");
     k.line("const sanic_u32x4 kv = kq[ps][v8];");
-    k.line("const float kf[8] = {__uint_as_float(kv.x << 16), __uint_as_float(kv.x & 0xFFFF0000u), __uint_as_float(kv.y << 16), __uint_as_float(kv.y & 0xFFFF0000u), __uint_as_float(kv.z << 16), __uint_as_float(kv.z & 0xFFFF0000u), __uint_as_float(kv.w << 16), __uint_as_float(kv.w & 0xFFFF0000u)};");
+    k.line(std::string(wk ? "" : "const ") + "float kf[8] = {__uint_as_float(kv.x << 16), __uint_as_float(kv.x & 0xFFFF0000u), __uint_as_float(kv.y << 16), __uint_as_float(kv.y & 0xFFFF0000u), __uint_as_float(kv.z << 16), __uint_as_float(kv.z & 0xFFFF0000u), __uint_as_float(kv.w << 16), __uint_as_float(kv.w & 0xFFFF0000u)};");
+    if (wk) {
+        k.line("if (kwriter && t == krow) {");
+        k.line("  #pragma unroll");
+        k.line("  for (int j = 0; j < 8; ++j) kf[j] = knew_lds[d0 + j];");
+        k.line("}");
+    }
     k.line("#pragma unroll");
     k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r)");
     k.line("  #pragma unroll");
@@ -418,7 +558,8 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("  const unsigned vw[8] = {vq[sb][0].x, vq[sb][0].y, vq[sb][0].z, vq[sb][0].w, vq[sb][1].x, vq[sb][1].y, vq[sb][1].z, vq[sb][1].w};");
         k.line("  #pragma unroll");
         k.line("  for (int j = 0; j < 16; ++j) {");
-        k.line("    const float vf = __uint_as_float((j & 1) ? (vw[j >> 1] & 0xFFFF0000u) : (vw[j >> 1] << 16));");
+        k.line(std::string("    ") + (wvv ? "" : "const ") + "float vf = __uint_as_float((j & 1) ? (vw[j >> 1] & 0xFFFF0000u) : (vw[j >> 1] << 16));");
+        if (wvv) k.line("    if (vwriter && t0 + tbase + j == vrow) vf = vnew_lds[e];");
         k.line("    #pragma unroll");
         k.line("    for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = fmaf(p_lds[r][tbase + j], vf, o[r]);");
         k.line("  }");
@@ -426,7 +567,8 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("  for (int j = 0; j < 16; ++j) {");
         k.line("    const idx_t t = t0 + tbase + j;");
         k.line("    if (t < t1) {");
-        k.line("      const float vf = sanic_bf16(vp[e * " + std::to_string(ve) + " + t]);");
+        k.line(std::string("      ") + (wvv ? "" : "const ") + "float vf = sanic_bf16(vp[e * " + std::to_string(ve) + " + t]);");
+        if (wvv) k.line("      if (vwriter && t == vrow) vf = vnew_lds[e];");
         k.line("      for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = fmaf(p_lds[r][tbase + j], vf, o[r]);");
         k.line("    }");
         k.line("  }");
@@ -435,7 +577,8 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("for (int j = 0; j < 16; ++j) {");
         k.line("  const idx_t t = t0 + tbase + j;");
         k.line("  if (t < t1) {");
-        k.line("    const float vf = sanic_bf16(vp[e * " + std::to_string(ve) + " + t * " + std::to_string(vt) + "]);");
+        k.line(std::string("    ") + (wvv ? "" : "const ") + "float vf = sanic_bf16(vp[e * " + std::to_string(ve) + " + t * " + std::to_string(vt) + "]);");
+        if (wvv) k.line("    if (vwriter && t == vrow) vf = vnew_lds[e];");
         k.line("    for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = fmaf(p_lds[r][tbase + j], vf, o[r]);");
         k.line("  }");
         k.line("}");
@@ -549,7 +692,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     std::ostringstream src;
     src << kPrelude << R.args_struct({"float* __restrict__ scratch"});
     src << "extern \"C\" __global__ void __launch_bounds__(256) " << kpart << "(Args a) {\n" << R.entry() << k.str() << "}\n";
-    out.kernel_kind = "skeleton:attn_decode[rep " + std::to_string(REP) + "]";
+    out.kernel_kind = "skeleton:attn_decode[rep " + std::to_string(REP) + "]" + (writes.empty() ? "" : "+writes" + std::to_string(writes.size()));
     out.source = src.str();
     std::vector<Arg> args = R.arg_list();
     args.push_back({Arg::SCRATCH, 0});

@@ -193,7 +193,7 @@ static int64_t vol(const int64_t* s, int r) {
     return v;
 }
 
-static void collect_inputs(const sanic_program_desc* d, int node, std::set<int>& bufs) {
+void collect_inputs(const sanic_program_desc* d, int node, std::set<int>& bufs) {
     const sanic_node& n = d->nodes[node];
     if (n.kind == SANIC_NODE_INPUT) bufs.insert(n.buffer);
     for (int k = 0; k < n.n_in; k++) collect_inputs(d, n.in[k], bufs);
@@ -432,7 +432,7 @@ static std::string gemv_prologue(Renderer& R, const sanic_program_desc* d, const
     return pc.str();
 }
 
-static void gemv_finish(Renderer& R, Code& code, const sanic_program_desc* d, const GemvPlan& P, bool coherent) {
+static std::string gemv_finish(Renderer& R, Code& code, const sanic_program_desc* d, const GemvPlan& P, bool coherent) {
     const sanic_stage& st = d->stages[P.stage];
     const sanic_carrier& c = st.carrier;
     for (size_t i = 0; i < P.cslots.size(); i++)
@@ -451,6 +451,31 @@ static void gemv_finish(Renderer& R, Code& code, const sanic_program_desc* d, co
         R.memo.pop_back();
     }
     code.line(store_stmt(R.param(st.out_buffer), "nn", st.out_dtype, v, coherent));
+    return v;
+}
+
+// A pointwise stage right after a batched group whose value is elementwise over the group's
+// outputs at its own index (e.g. silu(gate)·up): only MAP / CONST / INPUT nodes, every rank-1
+// input of extent N. Computed in the group kernel itself when each wave holds row i of every
+// segment, so the product never takes a launch or a re-read.
+static bool paired_candidate(const sanic_program_desc* d, int si, int64_t N) {
+    if (si >= d->n_stages) return false;
+    const sanic_stage& st = d->stages[si];
+    if (st.kind != SANIC_STAGE_POINTWISE || st.where >= 0 || st.rank != 1 || st.grid[0] != N) return false;
+    if (d->buffers[st.out_buffer].role == SANIC_BUF_STATE || d->buffers[st.out_buffer].role == SANIC_BUF_INPUT) return false;
+    std::vector<int> stack{st.value};
+    while (!stack.empty()) {
+        const sanic_node& n = d->nodes[stack.back()];
+        stack.pop_back();
+        if (n.kind == SANIC_NODE_CONST) continue;
+        if (n.kind == SANIC_NODE_INPUT) {
+            if (n.rank > 1 || (n.rank == 1 && n.shape[0] != N)) return false;
+            continue;
+        }
+        if (n.kind != SANIC_NODE_MAP) return false;
+        for (int k = 0; k < n.n_in; k++) stack.push_back(n.in[k]);
+    }
+    return true;
 }
 
 // ───────────────────────── in-place row write (emit_metal.rs:1103-1178) ───────────────────
@@ -467,7 +492,7 @@ static bool scalar_tree(const sanic_program_desc* d, int node) {
 }
 
 // match Lt(coord_dim, X + 1) where X is scalar: returns dim and X
-static bool match_row_cond(const sanic_program_desc* d, int node, int rank, int& dim, int& pos) {
+bool match_row_cond(const sanic_program_desc* d, int node, int rank, int& dim, int& pos) {
     const sanic_node& n = d->nodes[node];
     if (n.kind != SANIC_NODE_MAP) return false;
     if (n.op == SANIC_OP_MUL)
@@ -544,6 +569,7 @@ bool tail_candidate(const sanic_program_desc* d, int si) {
     if (si >= d->n_stages) return false;
     const sanic_stage& st = d->stages[si];
     if (st.kind != SANIC_STAGE_POINTWISE) return false;
+    if (attn_absorber(d, si) >= 0) return false;     // the attention kernel performs it
     int dim, pos;
     return pointwise_work(d, si, dim, pos) <= 65536;
 }
@@ -615,9 +641,23 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         group.push_back(P);
         seg_wbufs.push_back(wb);
     }
+    // an elementwise consumer of the whole group, computed per row pair in the kernel
+    int paired = -1;
+    {
+        bool same = group.size() >= 2;
+        for (auto& P : group) same = same && P.N == P0.N;
+        if (same && !getenv("SANIC_HIP_NO_PAIR") && paired_candidate(d, si + (int)group.size(), P0.N)) paired = si + (int)group.size();
+        if (paired >= 0) {
+            // it may read only group outputs and buffers nobody in the group writes
+            std::set<int> reads;
+            collect_inputs(d, d->stages[paired].value, reads);
+            for (int b : reads)
+                if (!written.count(b) && d->buffers[b].role != SANIC_BUF_INPUT && d->buffers[b].role != SANIC_BUF_STATE) paired = -1;
+        }
+    }
     // absorb the small pointwise stages that follow as the kernel's tail
     std::vector<int> tails;
-    for (int s = si + (int)group.size(); tail_candidate(d, s) && tails.size() < 4; s++) tails.push_back(s);
+    for (int s = si + (int)group.size() + (paired >= 0); tail_candidate(d, s) && tails.size() < 4; s++) tails.push_back(s);
 
     Renderer R(d);
     std::string prologue = gemv_prologue(R, d, P0);
@@ -630,6 +670,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
     const int KI = (int)((K + 511) / 512);
     int RQ = K <= 2048 ? 2 : 1;                  // rows in flight per wave iteration
     if (const char* e = getenv("SANIC_GEMV_RQ")) RQ = std::max(1, std::min(4, atoi(e)));
+    if (paired >= 0) RQ = (int)group.size();     // row i of every segment in one wave
     int64_t waves = (NTOT + RQ - 1) / RQ;
     int64_t max_blocks = 1024;
     if (const char* e = getenv("SANIC_GEMV_BLOCKS")) max_blocks = std::max(1, atoi(e));
@@ -652,7 +693,10 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
     auto setup = [&](Code& c) {
         for (int q = 0; q < RQ; q++) {
             std::string qs = std::to_string(q);
-            c.line("const idx_t row" + qs + " = r0 + " + qs + ";");
+            if (paired >= 0)
+                c.line("const idx_t row" + qs + " = r0 / " + std::to_string(RQ) + " + " + std::to_string(q * P0.N) + ";");
+            else
+                c.line("const idx_t row" + qs + " = r0 + " + qs + ";");
             c.line("const bool live" + qs + " = row" + qs + " < " + std::to_string(NTOT) + ";");
             c.line("int seg" + qs + " = 0;");
             for (size_t g = 1; g < group.size(); g++)
@@ -727,6 +771,55 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         }
     };
     auto finish = [&](Code& c) {
+        if (paired >= 0) {
+            for (int q = 0; q < RQ; q++)
+                for (int cs = 0; cs < SC; cs++) {
+                    std::string a = "acc" + std::to_string(q) + "_" + std::to_string(cs);
+                    c.line("for (int off = 32; off > 0; off >>= 1) " + a + " += __shfl_xor(" + a + ", off, 64);");
+                }
+            c.line("if (lane == 0 && live0) {");
+            c.indent++;
+            c.line("const idx_t wi = nn0;");
+            const sanic_stage& pst = d->stages[paired];
+            std::map<int, std::string> outv;      // segment output buffer -> its value in this wave
+            for (int q = 0; q < RQ; q++) {
+                std::string qs = std::to_string(q);
+                c.line("float pv" + qs + ";");
+                c.line("{");
+                c.indent++;
+                c.line("const idx_t nn = nn" + qs + ";");
+                std::string arr = "const float accq[" + std::to_string(SC) + "] = {";
+                for (int cs = 0; cs < SC; cs++) arr += (cs ? ", acc" : "acc") + qs + "_" + std::to_string(cs);
+                c.line(arr + "};");
+                R.memo.emplace_back();
+                std::string v = gemv_finish(R, c, d, group[q], !tails.empty());
+                R.memo.pop_back();
+                c.line("pv" + qs + " = " + v + ";");
+                c.indent--;
+                c.line("}");
+                outv[d->stages[group[q].stage].out_buffer] = "pv" + qs;
+            }
+            // the consumer's inputs that are group outputs read this wave's values
+            std::vector<int> stack{pst.value};
+            while (!stack.empty()) {
+                int ni = stack.back();
+                stack.pop_back();
+                const sanic_node& n = d->nodes[ni];
+                if (n.kind == SANIC_NODE_INPUT) {
+                    auto it = outv.find(n.buffer);
+                    if (it != outv.end()) R.subst[ni] = it->second;
+                }
+                for (int kk = 0; kk < n.n_in; kk++) stack.push_back(n.in[kk]);
+            }
+            R.memo.emplace_back();
+            std::string pv = R.value(c, pst.value, {"wi"});
+            R.memo.pop_back();
+            R.subst.clear();
+            c.line(store_stmt(R.param(pst.out_buffer), "wi", pst.out_dtype, pv, !tails.empty()));
+            c.indent--;
+            c.line("}");
+            return;
+        }
         for (int q = 0; q < RQ; q++)
             for (int cs = 0; cs < SC; cs++) {
                 std::string a = "acc" + std::to_string(q) + "_" + std::to_string(cs);
@@ -811,6 +904,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     LoweredStage L;
     L.kernel_kind = "skeleton:gemv" + std::string(group.size() > 1 ? "[batched " + std::to_string(group.size()) + "]" : "") +
+                    (paired >= 0 ? "+paired" : "") +
                     (tails.empty() ? "" : "+tail" + std::to_string(tails.size()));
     L.source = src.str();
     uint32_t lds = (uint32_t)((SC * K + 4 * std::max(SR, 1)) * 4);
@@ -821,6 +915,11 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
     for (size_t g = 1; g < group.size(); g++) {
         LoweredStage B;
         B.kernel_kind = "batched-into:" + std::to_string(si);
+        out.push_back(std::move(B));
+    }
+    if (paired >= 0) {
+        LoweredStage B;
+        B.kernel_kind = "paired-into:" + std::to_string(si);
         out.push_back(std::move(B));
     }
     for (size_t t = 0; t < tails.size(); t++) {

@@ -1,5 +1,6 @@
 // Structural analysis shared by the skeletons: symbolic affine coordinates and accesses.
 #pragma once
+#include <set>
 #include <string>
 #include <vector>
 
@@ -37,6 +38,13 @@ bool sym_access(const sanic_program_desc* d, int node, const std::vector<Sym>& c
 
 bool sym_child_coords(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
                       const std::vector<int64_t>& ext, std::vector<Sym>& sc);
+
+void collect_inputs(const sanic_program_desc* d, int node, std::set<int>& bufs);
+// match Lt(coordinate, X + 1) (inside a product) with X scalar: the row dim and X's node
+bool match_row_cond(const sanic_program_desc* d, int node, int rank, int& dim, int& pos);
+// The decode-attention stage that performs in-place row write `si` itself (the K/V cache
+// update of this step feeding that attention), or -1.
+int attn_absorber(const sanic_program_desc* d, int si);
 
 bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out);
 bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out);

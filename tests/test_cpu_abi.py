@@ -42,7 +42,8 @@ def test_open_without_gpu_reports_backend_error():
     assert st == 6 and not h.value   # SANIC_ERR_BACKEND (MetalDevice::open → None)
 
 
-@pytest.mark.parametrize("name", ["A", "A_coop", "A_split", "B1", "B1_rows", "D1", "C3", "E_stage"])
+@pytest.mark.parametrize("name", ["A", "A_coop", "A_split", "B1", "B1_rows", "B2", "D1", "D2", "C1", "C3",
+                                  "E_qkv", "E_attn", "E_gateup"])
 def test_lowering_chooses_the_expected_kernel(name):
     progs = {
         "A": (configs.direct_attention(), 0, "fold:scalar"),
@@ -52,7 +53,14 @@ def test_lowering_chooses_the_expected_kernel(name):
         "B1_rows": (configs.rmsnorm_projection(kmajor=False), 0, "skeleton:gemv"),
         "D1": (configs.int4_matmul(), 0, "skeleton:gemv"),
         "C3": (configs.decode_attention(), 0, "skeleton:attn_decode"),
-        "E_stage": (configs.llama_decode(), 1, "skeleton:gemv[batched 3]+tail2"),
+        "B2": (configs.rmsnorm_projection(M=512), 0, "skeleton:gemm[128x128,a2]"),
+        "D2": (configs.int4_matmul(M=128), 0, "skeleton:gemm"),
+        "C1": (configs.flash_prefill(), 2, "skeleton:flash_prefill"),
+        # q/k/v batched into one launch; this step's K/V cache writes done by the attention kernel
+        "E_qkv": (configs.llama_decode(), 1, "skeleton:gemv[batched 3]"),
+        "E_attn": (configs.llama_decode(), 6, "skeleton:attn_decode[rep 4]+writes2"),
+        # gate/up batched with silu(gate)·up computed per row pair
+        "E_gateup": (configs.llama_decode(), 8, "skeleton:gemv[batched 2]+paired"),
     }
     p, stage, want = progs[name]
     kind, src = p.emit(stage)
