@@ -323,11 +323,14 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const int REP = P.rep;
     const int64_t HD = P.dot.depth, E = P.E, T = P.T, NH = P.NH;
     const int64_t NG = NH / REP;
-    int CH = 256;                                 // stream positions per workgroup
-    if (const char* e = getenv("SANIC_ATTN_CH")) CH = std::max(64, std::min(1024, atoi(e) / 64 * 64));
-    const int64_t NCH = (T + CH - 1) / CH;
     const int NS = (int)P.scalar_slots.size(), NV = (int)P.vec_slots.size();
     const int PSZ = 1 + NS + NV * (int)E;         // floats per (chunk, head) partial
+    // stream positions per workgroup: 64 (many small workgroups, short phases), doubled until
+    // one group's partials fit the merging workgroup's LDS
+    int CH = 64;
+    while (CH < 1024 && ((T + CH - 1) / CH) * REP * PSZ * 4 > 40 * 1024) CH *= 2;
+    if (const char* e = getenv("SANIC_ATTN_CH")) CH = std::max(64, std::min(1024, atoi(e) / 64 * 64));
+    const int64_t NCH = (T + CH - 1) / CH;
     int64_t part_off = scratch;
     scratch += ((NCH * NH * PSZ * 4 + 255) / 256) * 256;
 
@@ -534,7 +537,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));");
     k.line("float l = 0.0f;");
     k.line("for (int i = lane; i < " + std::to_string(CH) + "; i += 64) {");
-    k.line("  const float p = m == (-__builtin_huge_valf()) ? 0.0f : expf(p_lds[r][i] - m);");
+    k.line("  const float p = m == (-__builtin_huge_valf()) ? 0.0f : __builtin_amdgcn_exp2f((p_lds[r][i] - m) * 1.44269504088896341f);");
     k.line("  p_lds[r][i] = p;");
     k.line("  l += p;");
     k.line("}");
@@ -605,12 +608,14 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
 
     k.line("}  // visible chunk");
     // Merge, fused: the last workgroup of this KV group to finish stages the group's partials in
-    // LDS and folds them per output point with the carrier's rendered combine (program order is
-    // that of run_carrier_split: chunk 0 first), then projects, runs the epilogue and stores.
+    // LDS and merges them in one n-way step of the ExpShifted combine (derive.rs:1688-1747
+    // applied to all chunks at once): M = max_c m_c, w_c = [−∞ < m_c]·exp(m_c − M), every
+    // ExpShifted slot = Σ_c w_c·x_c. This is the pairwise combine of run_carrier_split
+    // (interp.rs:555-643) regrouped — no chain of NCH dependent steps.
     int64_t counter_off = scratch;
     scratch += ((NG * 4 + 255) / 256) * 256;
     const int64_t GP = NCH * REP * PSZ;       // floats of one group's partials
-    const bool in_lds = GP * 4 <= 48 * 1024;
+    if (GP * 4 > 64 * 1024) return false;
     k.line("{");
     k.indent++;
     k.line("__shared__ int sanic_last;");
@@ -620,23 +625,41 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("if (tid == 0) sanic_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == " + std::to_string(NCH) + "u - 1u;");
     k.line("__syncthreads();");
     k.line("if (!sanic_last) return;");
-    std::string src_expr;   // partial (chunk ch, head-in-group r, field f)
-    if (in_lds) {
-        k.line("__shared__ float g_lds[" + std::to_string(GP) + "];");
-        k.line("for (int i = tid; i < " + std::to_string(GP) + "; i += 256) {");
-        k.line("  const int ch = i / " + std::to_string(REP * PSZ) + ", rem = i % " + std::to_string(REP * PSZ) + ";");
-        k.line("  g_lds[i] = sanic_ld(a.scratch + " + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + ") * " + std::to_string(PSZ) + " + rem);");
-        k.line("}");
-        k.line("__syncthreads();");
-        src_expr = "g_lds[(ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + " + FIELD]";
-    } else {
-        src_expr = "sanic_ld(a.scratch + " + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + " + FIELD)";
-    }
+    k.line("__shared__ float g_lds[" + std::to_string(GP) + "];");
+    k.line("__shared__ float w_lds[" + std::to_string(REP) + "][" + std::to_string(NCH) + "];");
+    k.line("__shared__ float mx_lds[" + std::to_string(REP) + "];");
+    // every coherent load is issued before the first is consumed (one round trip, not GP/256)
+    const int64_t PER = (GP + 255) / 256;
+    k.line("float gv[" + std::to_string(PER) + "];");
+    k.line("#pragma unroll");
+    k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j) {");
+    k.line("  const int i = tid + j * 256;");
+    k.line("  const int ch = i / " + std::to_string(REP * PSZ) + ", rem = i % " + std::to_string(REP * PSZ) + ";");
+    k.line("  gv[j] = i < " + std::to_string(GP) + " ? sanic_ld(a.scratch + " + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " +
+           std::to_string(REP) + ") * " + std::to_string(PSZ) + " + rem) : 0.0f;");
+    k.line("}");
+    k.line("#pragma unroll");
+    k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j)");
+    k.line("  if (tid + j * 256 < " + std::to_string(GP) + ") g_lds[tid + j * 256] = gv[j];");
+    k.line("__syncthreads();");
     k.line("if (tid == 0) sanic_st(cnt, 0u);");
+    // per head (one wave each): M and the chunk weights
+    k.line("for (int r = wv; r < " + std::to_string(REP) + "; r += 4) {");
+    k.indent++;
+    k.line("float m = (-__builtin_huge_valf());");
+    k.line("for (int ch = lane; ch < " + std::to_string(NCH) + "; ch += 64) m = fmaxf(m, g_lds[(ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + "]);");
+    k.line("for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));");
+    k.line("for (int ch = lane; ch < " + std::to_string(NCH) + "; ch += 64) {");
+    k.line("  const float mc = g_lds[(ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + "];");
+    k.line("  w_lds[r][ch] = (-__builtin_huge_valf()) < mc ? __builtin_amdgcn_exp2f((mc - m) * 1.44269504088896341f) : 0.0f;");
+    k.line("}");
+    k.line("if (lane == 0) mx_lds[r] = m;");
+    k.indent--;
+    k.line("}");
+    k.line("__syncthreads();");
     k.line("for (int pt = tid; pt < " + std::to_string(REP * E) + "; pt += 256) {");
     k.indent++;
     k.line("const int r = pt / " + std::to_string(E) + ", ee = pt % " + std::to_string(E) + ";");
-    // grid coordinates of this output point
     for (int j = 0; j < st.rank; j++) {
         std::string v = j == P.hdim ? "(grp * " + std::to_string(REP) + " + r)" : j == P.edim ? "(idx_t)ee" : "0";
         k.line("const idx_t g" + std::to_string(j) + " = " + v + ";");
@@ -646,29 +669,23 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         lin = j == 0 ? "g0" : "(" + lin + " * " + std::to_string(st.grid[j]) + " + g" + std::to_string(j) + ")";
     k.line("const idx_t gid = " + lin + ";");
     auto field = [&](int slot) -> std::string {
-        if (slot == P.max_slot) return "0";
         for (int sidx = 0; sidx < NS; sidx++) if (P.scalar_slots[sidx] == slot) return std::to_string(1 + sidx);
         for (int v = 0; v < NV; v++) if (P.vec_slots[v] == slot) return std::to_string(1 + NS + v * E) + " + ee";
         return "0";
     };
-    auto at = [&](const std::string& ch, int slot) {
-        std::string e = src_expr;
-        e.replace(e.find("ch *"), 2, ch);
-        e.replace(e.find("FIELD"), 5, field(slot));
-        return e;
-    };
-    for (int sidx = 0; sidx < c.slots; sidx++) k.line("float acc" + std::to_string(sidx) + " = " + at("0", sidx) + ";");
-    k.line("for (int ch = 1; ch < " + std::to_string(NCH) + "; ++ch) {");
-    k.indent++;
-    for (int sidx = 0; sidx < c.slots; sidx++) k.line("const float o" + std::to_string(sidx) + " = " + at("ch", sidx) + ";");
-    R.memo.emplace_back();
     for (int sidx = 0; sidx < c.slots; sidx++) {
-        std::string v = R.expr(k, c.combine[sidx], "", "acc", "o", "");
-        k.line("const float nx" + std::to_string(sidx) + " = " + v + ";");
+        std::string ss = std::to_string(sidx);
+        if (sidx == P.max_slot) { k.line("const float acc" + ss + " = mx_lds[r];"); continue; }
+        k.line("float acc" + ss + " = 0.0f;");
     }
-    R.memo.pop_back();
-    for (int sidx = 0; sidx < c.slots; sidx++) k.line("acc" + std::to_string(sidx) + " = nx" + std::to_string(sidx) + ";");
-    k.indent--;
+    k.line("for (int ch = 0; ch < " + std::to_string(NCH) + "; ++ch) {");
+    k.line("  const float wc = w_lds[r][ch];");
+    k.line("  const float* pc = g_lds + (ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + ";");
+    for (int sidx = 0; sidx < c.slots; sidx++) {
+        if (sidx == P.max_slot) continue;
+        std::string ss = std::to_string(sidx);
+        k.line("  acc" + ss + " = fmaf(wc, pc[" + field(sidx) + "], acc" + ss + ");");
+    }
     k.line("}");
     R.memo.emplace_back();
     std::string f = R.expr(k, c.project, "", "", "", "acc");

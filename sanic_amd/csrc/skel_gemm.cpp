@@ -128,7 +128,8 @@ bool gemm_plan(const sanic_program_desc* d, int si, GemmPlan& P) {
 std::vector<std::string> render_weight_run(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
                                            const std::vector<int64_t>& ext, Code& lc, Code& dc, const std::string& nn,
                                            const std::string& k0, const std::string& sfx, std::vector<int>& bufs,
-                                           std::vector<int>& dtypes, bool& ok, bool& contiguous, std::string& raw_bf16);
+                                           std::vector<int>& dtypes, bool& ok, bool& contiguous, std::string& raw_bf16,
+                                           bool stream);
 
 bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
     (void)scratch;
@@ -179,7 +180,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     std::string raw;
     {
         Code l1, d1;
-        render_weight_run(d, st.leaf[P.w], cw, {N, K}, l1, d1, "nn", "k0", "_p", wbufs, wdts, ok, contig, raw);
+        render_weight_run(d, st.leaf[P.w], cw, {N, K}, l1, d1, "nn", "k0", "_p", wbufs, wdts, ok, contig, raw, false);
         if (!ok) return false;
     }
     // row leaves vector forms over vars {0: m, 1: k}
@@ -195,7 +196,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         bool rok = true, rc = true;
         std::string rr;
         Code l1, d1;
-        render_weight_run(d, st.leaf[l], cr, {M, K}, l1, d1, "mm", "k0", "_p", rb, rd, rok, rc, rr);
+        render_weight_run(d, st.leaf[l], cr, {M, K}, l1, d1, "mm", "k0", "_p", rb, rd, rok, rc, rr, false);
         if (!rok || !rc) return false;
         crow.push_back(cr);
     }
@@ -238,7 +239,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
                 Code l1, d1;
                 l1.indent = d1.indent = c2.indent;
                 auto vals = render_weight_run(d, st.leaf[P.rows[li]], crow[li], {M, K}, l1, d1, "mm" + sfx, k0,
-                                              "_a" + std::to_string(li) + "_" + std::to_string(r) + sfx, rb, rd, rok, rc, rr);
+                                              "_a" + std::to_string(li) + "_" + std::to_string(r) + sfx, rb, rd, rok, rc, rr, false);
                 for (size_t b = 0; b < rb.size(); b++)
                     c2.line("const " + std::string(ctype_of(rd[b])) + "* __restrict__ wb" + std::to_string(b) + "_a" + std::to_string(li) + "_" + std::to_string(r) + sfx + " = " + R.param(rb[b]) + ";");
                 c2.s << l1.str() << d1.str();
@@ -262,7 +263,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             std::string rr;
             Code l1, d1;
             l1.indent = d1.indent = c2.indent;
-            auto vals = render_weight_run(d, st.leaf[P.w], cw, {N, K}, l1, d1, nn, kk, "_b" + rs + sfx, rb, rd, rok, rc, rr);
+            auto vals = render_weight_run(d, st.leaf[P.w], cw, {N, K}, l1, d1, nn, kk, "_b" + rs + sfx, rb, rd, rok, rc, rr, false);
             for (size_t b = 0; b < rb.size(); b++)
                 c2.line("const " + std::string(ctype_of(rd[b])) + "* __restrict__ wb" + std::to_string(b) + "_b" + rs + sfx + " = " + R.param(rb[b]) + ";");
             c2.s << l1.str();

@@ -216,6 +216,10 @@ struct VecW {
     bool contiguous = true;       // every access moves by 0 or 1 element along k
     std::string nn = "nn", k0 = "k0", ptr = "wb", psfx, sfx;
     std::string last_raw;     // the 128-bit bf16 register of the last contiguous access
+    bool stream = true;           // weights are read once: non-temporal loads
+    std::string ld(const std::string& ty, const std::string& ptr) const {
+        return stream ? "__builtin_nontemporal_load((const " + ty + "*)(" + ptr + "))" : "*(const " + ty + "*)(" + ptr + ")";
+    }
     std::string fresh(const char* p) { return std::string(p) + std::to_string(tmp++) + sfx; }
 
     std::vector<std::string> render(Code& lc, Code& dc, int node, const std::vector<Sym>& c, const std::vector<int64_t>& ext) {
@@ -280,7 +284,7 @@ struct VecW {
         }
         if (jstride == 1 && acc.dtype == SANIC_BF16) {
             std::string v = fresh("wq");
-            lc.line("const sanic_u32x4 " + v + " = __builtin_nontemporal_load((const sanic_u32x4*)(" + p + " + " + base + "));");
+            lc.line("const sanic_u32x4 " + v + " = " + ld("sanic_u32x4", p + " + " + base) + ";");
             last_raw = v;
             for (int j = 0; j < 8; j++)
                 out[j] = std::string("__uint_as_float(") + (j % 2 == 0 ? "(" + v + "." + comp[j / 2] + " << 16)"
@@ -289,14 +293,14 @@ struct VecW {
         }
         if (jstride == 1 && acc.dtype == SANIC_F32) {
             std::string v0 = fresh("f"), v1 = fresh("f");
-            lc.line("const sanic_f32x4 " + v0 + " = __builtin_nontemporal_load((const sanic_f32x4*)(" + p + " + " + base + "));");
-            lc.line("const sanic_f32x4 " + v1 + " = __builtin_nontemporal_load((const sanic_f32x4*)(" + p + " + " + base + " + 4));");
+            lc.line("const sanic_f32x4 " + v0 + " = " + ld("sanic_f32x4", p + " + " + base) + ";");
+            lc.line("const sanic_f32x4 " + v1 + " = " + ld("sanic_f32x4", p + " + " + base + " + 4") + ";");
             for (int j = 0; j < 8; j++) out[j] = (j < 4 ? v0 : v1) + "." + comp[j % 4];
             return out;
         }
         if (jstride == 1 && (acc.dtype == SANIC_U4 || acc.dtype == SANIC_I4)) {
             std::string v = fresh("u");
-            lc.line("const unsigned " + v + " = __builtin_nontemporal_load((const unsigned*)(" + p + " + (" + base + " >> 1)));");
+            lc.line("const unsigned " + v + " = " + ld("unsigned", p + " + (" + base + " >> 1)") + ";");
             for (int j = 0; j < 8; j++) {
                 std::string e = "(float)((" + v + " >> " + std::to_string(4 * j) + ") & 0xFu)";
                 out[j] = acc.dtype == SANIC_I4 ? "(" + e + " - 8.0f)" : e;
@@ -317,8 +321,10 @@ struct VecW {
 std::vector<std::string> render_weight_run(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
                                            const std::vector<int64_t>& ext, Code& lc, Code& dc, const std::string& nn,
                                            const std::string& k0, const std::string& sfx, std::vector<int>& bufs,
-                                           std::vector<int>& dtypes, bool& ok, bool& contiguous, std::string& raw_bf16) {
+                                           std::vector<int>& dtypes, bool& ok, bool& contiguous, std::string& raw_bf16,
+                                           bool stream) {
     VecW vw{d};
+    vw.stream = stream;
     vw.nn = nn;
     vw.k0 = k0;
     vw.ptr = "wb";
@@ -679,6 +685,237 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
     if (!tails.empty()) {
         counter_off = scratch;
         scratch += 256;
+    }
+
+    // ── split-K form: the 4 waves of a workgroup take one quarter of K each, every lane keeps
+    // its activation factors in registers (loaded once, reused by all rows of the workgroup),
+    // and the per-wave partials meet in LDS once at the end: no LDS staging of the activation
+    // and no barrier before the weight FMAs.
+    if (K % 2048 == 0 && K <= 16384 && !getenv("SANIC_GEMV_V1")) {
+        const int64_t KQ = K / 4;
+        const int KIq = (int)(KQ / 512);
+        const int NSEG = (int)group.size();
+        int RBI = K >= 8192 ? 4 : 2;
+        if (const char* e = getenv("SANIC_GEMV_RB")) RBI = std::max(1, std::min(8, atoi(e)));
+        if (paired >= 0) RBI = 1;
+        const int RB = paired >= 0 ? NSEG : RBI;                 // rows per workgroup
+        const int64_t UNITS = paired >= 0 ? P0.N : NTOT;
+        const int64_t nblocks = (UNITS + RBI - 1) / RBI;
+        const int RW = RB * SC + SR;                             // partials per wave
+        Code k;
+        k.indent = 1;
+        k.line("__shared__ float red[4][" + std::to_string(RW) + "];");
+        k.line("const int t = threadIdx.x, lane = t & 63, wv = t >> 6;");
+        k.line("const idx_t kb = (idx_t)wv * " + std::to_string(KQ) + ";");
+        // rows of this workgroup
+        for (int q = 0; q < RB; q++) {
+            std::string qs = std::to_string(q);
+            if (paired >= 0) {
+                k.line("const idx_t row" + qs + " = (idx_t)blockIdx.x + " + std::to_string(q * P0.N) + ";");
+                k.line("const bool live" + qs + " = (idx_t)blockIdx.x < " + std::to_string(P0.N) + ";");
+                k.line("const int seg" + qs + " = " + qs + ";");
+                k.line("const idx_t nn" + qs + " = live" + qs + " ? (idx_t)blockIdx.x : 0;");
+                for (size_t b = 0; b < wb0.size(); b++)
+                    k.line("const " + std::string(ctype_of(wd0[b])) + "* __restrict__ wb" + std::to_string(b) + "_" + qs + " = " + R.param(seg_wbufs[q][b]) + ";");
+                continue;
+            }
+            k.line("const idx_t row" + qs + " = (idx_t)blockIdx.x * " + std::to_string(RBI) + " + " + qs + ";");
+            k.line("const bool live" + qs + " = row" + qs + " < " + std::to_string(NTOT) + ";");
+            k.line("int seg" + qs + " = 0;");
+            for (size_t g = 1; g < group.size(); g++)
+                k.line("if (row" + qs + " >= " + std::to_string(seg_off[g]) + ") seg" + qs + " = " + std::to_string(g) + ";");
+            std::string nnexpr = "row" + qs;
+            for (size_t g = 1; g < group.size(); g++)
+                nnexpr = "(seg" + qs + " == " + std::to_string(g) + " ? row" + qs + " - " + std::to_string(seg_off[g]) + " : " + nnexpr + ")";
+            k.line("const idx_t nn" + qs + " = live" + qs + " ? " + nnexpr + " : 0;");
+            for (size_t b = 0; b < wb0.size(); b++) {
+                std::string sel = R.param(seg_wbufs[0][b]);
+                for (size_t g = 1; g < group.size(); g++)
+                    sel = "(seg" + qs + " == " + std::to_string(g) + " ? " + R.param(seg_wbufs[g][b]) + " : " + sel + ")";
+                k.line("const " + std::string(ctype_of(wd0[b])) + "* __restrict__ wb" + std::to_string(b) + "_" + qs + " = " + sel + ";");
+            }
+        }
+        // weight loads: every (row, run) is requested before any arithmetic
+        std::vector<std::vector<std::vector<std::string>>> wvals(RB, std::vector<std::vector<std::string>>(KIq));
+        Code wdc;
+        wdc.indent = k.indent;
+        for (int q = 0; q < RB; q++)
+            for (int i = 0; i < KIq; i++) {
+                VecW vw{d};
+                vw.nn = "nn" + std::to_string(q);
+                vw.k0 = "(kb + " + std::to_string(i * 512) + " + lane * 8)";
+                vw.ptr = "wb";
+                vw.psfx = "_" + std::to_string(q);
+                vw.sfx = "_" + std::to_string(q) + "_" + std::to_string(i);
+                Code l1;
+                l1.indent = k.indent;
+                wvals[q][i] = vw.render(l1, wdc, d->stages[P0.stage].leaf[P0.w], weight_coords(d, d->stages[P0.stage], P0.w, P0.ndim), {P0.N, P0.K});
+                if (!vw.ok) return false;
+                k.s << l1.str();
+            }
+        // activation factors of this lane's k runs (loads, then arithmetic)
+        const sanic_stage& st0 = d->stages[P0.stage];
+        const sanic_carrier& c0 = st0.carrier;
+        std::vector<std::vector<std::vector<std::string>>> lvals(st0.n_leaves, std::vector<std::vector<std::string>>(KIq));
+        Code adc;
+        adc.indent = k.indent;
+        for (int l = 0; l < st0.n_leaves; l++) {
+            if (l == P0.w) continue;
+            const sanic_node& ln = d->nodes[st0.leaf[l]];
+            std::vector<Sym> cl(ln.rank);
+            for (int j = 0; j < ln.rank; j++) cl[j] = st0.bind[l][j] == SANIC_BIND_STREAM ? Sym::var(1) : Sym();
+            for (int i = 0; i < KIq; i++) {
+                VecW vw{d};
+                vw.stream = false;
+                vw.nn = "0";
+                vw.k0 = "(kb + " + std::to_string(i * 512) + " + lane * 8)";
+                vw.ptr = "xb";
+                vw.psfx = "_" + std::to_string(l) + "_" + std::to_string(i);
+                vw.sfx = "_x" + std::to_string(l) + "_" + std::to_string(i);
+                Code l1;
+                l1.indent = k.indent;
+                lvals[l][i] = vw.render(l1, adc, st0.leaf[l], cl, {1, P0.K});
+                if (!vw.ok) return false;
+                for (size_t b = 0; b < vw.bufs.size(); b++)
+                    k.line("const " + std::string(ctype_of(vw.dtypes[b])) + "* __restrict__ xb" + std::to_string(b) + vw.psfx + " = " + R.param(vw.bufs[b]) + ";");
+                k.s << l1.str();
+            }
+        }
+        k.s << adc.str() << wdc.str();
+        for (int r = 0; r < SR; r++) k.line("float rpart" + std::to_string(r) + " = 0.0f;");
+        for (int q = 0; q < RB; q++)
+            for (int cs = 0; cs < SC; cs++) k.line("float acc" + std::to_string(q) + "_" + std::to_string(cs) + " = 0.0f;");
+        for (int i = 0; i < KIq; i++)
+            for (int j = 0; j < 8; j++) {
+                std::string ij = std::to_string(i) + "_" + std::to_string(j);
+                for (int cs = 0; cs < SC; cs++) k.line("float af" + std::to_string(cs) + "_" + ij + ";");
+                k.line("{");
+                k.indent++;
+                R.memo.emplace_back();
+                for (int l = 0; l < st0.n_leaves; l++)
+                    if (l != P0.w) k.line("const float x" + std::to_string(l) + " = " + lvals[l][i][j] + ";");
+                for (int cs = 0; cs < SC; cs++)
+                    k.line("af" + std::to_string(cs) + "_" + ij + " = " + expr_without(R, k, c0.into[P0.cslots[cs]], P0.w, "x") + ";");
+                for (int r = 0; r < SR; r++)
+                    k.line("rpart" + std::to_string(r) + " += " + R.expr(k, c0.into[P0.rslots[r]], "x", "", "", "") + ";");
+                R.memo.pop_back();
+                k.indent--;
+                k.line("}");
+                for (int q = 0; q < RB; q++)
+                    for (int cs = 0; cs < SC; cs++) {
+                        std::string a = "acc" + std::to_string(q) + "_" + std::to_string(cs);
+                        k.line(a + " = fmaf(af" + std::to_string(cs) + "_" + ij + ", " + wvals[q][i][j] + ", " + a + ");");
+                    }
+            }
+        // wave partials -> LDS -> one thread per row finishes it
+        std::vector<std::string> parts;
+        for (int q = 0; q < RB; q++)
+            for (int cs = 0; cs < SC; cs++) parts.push_back("acc" + std::to_string(q) + "_" + std::to_string(cs));
+        for (int r = 0; r < SR; r++) parts.push_back("rpart" + std::to_string(r));
+        for (size_t i = 0; i < parts.size(); i++) {
+            k.line("for (int off = 32; off > 0; off >>= 1) " + parts[i] + " += __shfl_xor(" + parts[i] + ", off, 64);");
+        }
+        k.line("if (lane == 0) {");
+        for (size_t i = 0; i < parts.size(); i++) k.line("  red[wv][" + std::to_string(i) + "] = " + parts[i] + ";");
+        k.line("}");
+        k.line("__syncthreads();");
+        auto sum4 = [&](int i) {
+            std::string is = std::to_string(i);
+            return "((red[0][" + is + "] + red[1][" + is + "]) + red[2][" + is + "]) + red[3][" + is + "]";
+        };
+        auto finish_row = [&](Code& c, int q, int g) -> std::string {
+            std::string qs = std::to_string(q);
+            c.line("const idx_t nn = nn" + qs + ";");
+            std::string arr = "const float accq[" + std::to_string(SC) + "] = {";
+            for (int cs = 0; cs < SC; cs++) arr += (cs ? ", " : "") + sum4(q * SC + cs);
+            c.line(arr + "};");
+            for (int r = 0; r < SR; r++) c.line("const float racc" + std::to_string(r) + " = " + sum4(RB * SC + r) + ";");
+            R.memo.emplace_back();
+            std::string v = gemv_finish(R, c, d, group[g], !tails.empty());
+            R.memo.pop_back();
+            return v;
+        };
+        if (paired >= 0) {
+            k.line("if (t == 0 && live0) {");
+            k.indent++;
+            k.line("const idx_t wi = nn0;");
+            const sanic_stage& pst = d->stages[paired];
+            std::map<int, std::string> outv;
+            for (int q = 0; q < RB; q++) {
+                std::string qs = std::to_string(q);
+                k.line("float pv" + qs + ";");
+                k.line("{");
+                k.indent++;
+                std::string v = finish_row(k, q, q);
+                k.line("pv" + qs + " = " + v + ";");
+                k.indent--;
+                k.line("}");
+                outv[d->stages[group[q].stage].out_buffer] = "pv" + qs;
+            }
+            std::vector<int> stack{pst.value};
+            while (!stack.empty()) {
+                int ni = stack.back();
+                stack.pop_back();
+                const sanic_node& n = d->nodes[ni];
+                if (n.kind == SANIC_NODE_INPUT) {
+                    auto it = outv.find(n.buffer);
+                    if (it != outv.end()) R.subst[ni] = it->second;
+                }
+                for (int kk = 0; kk < n.n_in; kk++) stack.push_back(n.in[kk]);
+            }
+            R.memo.emplace_back();
+            std::string pv = R.value(k, pst.value, {"wi"});
+            R.memo.pop_back();
+            R.subst.clear();
+            k.line(store_stmt(R.param(pst.out_buffer), "wi", pst.out_dtype, pv, !tails.empty()));
+            k.indent--;
+            k.line("}");
+        } else {
+            for (int q = 0; q < RB; q++) {
+                std::string qs = std::to_string(q);
+                k.line("if (t == " + qs + " && live" + qs + ") {");
+                k.indent++;
+                for (size_t g = 0; g < group.size(); g++) {
+                    k.line(std::string(g ? "} else " : "") + "if (seg" + qs + " == " + std::to_string(g) + ") {");
+                    k.indent++;
+                    finish_row(k, q, (int)g);
+                    k.indent--;
+                }
+                k.line("}");
+                k.indent--;
+                k.line("}");
+            }
+        }
+        if (!tails.empty())
+            emit_tail(R, k, d, tails, "(unsigned*)((char*)a.scratch + " + std::to_string(counter_off) + ")", "gridDim.x");
+        const std::string kname = "sanic_gemv_" + std::to_string(NTOT) + "x" + std::to_string(K);
+        std::ostringstream src;
+        src << kPrelude << R.args_struct(tails.empty() ? std::vector<std::string>{} : std::vector<std::string>{"float* __restrict__ scratch"})
+            << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
+        LoweredStage L;
+        L.kernel_kind = "skeleton:gemv" + std::string(group.size() > 1 ? "[batched " + std::to_string(group.size()) + "]" : "") +
+                        (paired >= 0 ? "+paired" : "") + (tails.empty() ? "" : "+tail" + std::to_string(tails.size()));
+        L.source = src.str();
+        std::vector<Arg> args = R.arg_list();
+        if (!tails.empty()) args.push_back({Arg::SCRATCH, 0});
+        L.launches.push_back({kname, "", dim3((unsigned)nblocks), dim3(256), 0, args});
+        out.push_back(std::move(L));
+        for (size_t g = 1; g < group.size(); g++) {
+            LoweredStage B;
+            B.kernel_kind = "batched-into:" + std::to_string(si);
+            out.push_back(std::move(B));
+        }
+        if (paired >= 0) {
+            LoweredStage B;
+            B.kernel_kind = "paired-into:" + std::to_string(si);
+            out.push_back(std::move(B));
+        }
+        for (size_t t = 0; t < tails.size(); t++) {
+            LoweredStage B;
+            B.kernel_kind = "tail-of:" + std::to_string(si);
+            out.push_back(std::move(B));
+        }
+        return true;
     }
 
     Code k;
