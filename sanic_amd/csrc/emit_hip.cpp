@@ -264,6 +264,12 @@ __device__ __forceinline__ float sanic_u4(const unsigned char* p, idx_t i) {
 }
 // device-coherent (agent-scope) accesses for data exchanged between workgroups of one kernel:
 // written through to the level every XCD sees, read past the local L2
+// 16 bytes at base + off from the device-coherent level (the agent-scope atomics' cache
+// policy), as one buffer load the compiler can keep in flight with others
+__device__ __forceinline__ sanic_f32x4 sanic_ld4(const float* base, unsigned off_bytes) {
+  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, 0x7fffffff, 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off_bytes, 0, 16);
+}
 template <class T> __device__ __forceinline__ T sanic_ld(const T* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

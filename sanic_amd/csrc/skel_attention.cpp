@@ -625,22 +625,39 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("if (tid == 0) sanic_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == " + std::to_string(NCH) + "u - 1u;");
     k.line("__syncthreads();");
     k.line("if (!sanic_last) return;");
-    k.line("__shared__ float g_lds[" + std::to_string(GP) + "];");
+    k.line("__shared__ __attribute__((aligned(16))) float g_lds[" + std::to_string(GP) + "];");
     k.line("__shared__ float w_lds[" + std::to_string(REP) + "][" + std::to_string(NCH) + "];");
     k.line("__shared__ float mx_lds[" + std::to_string(REP) + "];");
-    // every coherent load is issued before the first is consumed (one round trip, not GP/256)
-    const int64_t PER = (GP + 255) / 256;
-    k.line("float gv[" + std::to_string(PER) + "];");
-    k.line("#pragma unroll");
-    k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j) {");
-    k.line("  const int i = tid + j * 256;");
-    k.line("  const int ch = i / " + std::to_string(REP * PSZ) + ", rem = i % " + std::to_string(REP * PSZ) + ";");
-    k.line("  gv[j] = i < " + std::to_string(GP) + " ? sanic_ld(a.scratch + " + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " +
-           std::to_string(REP) + ") * " + std::to_string(PSZ) + " + rem) : 0.0f;");
-    k.line("}");
-    k.line("#pragma unroll");
-    k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j)");
-    k.line("  if (tid + j * 256 < " + std::to_string(GP) + ") g_lds[tid + j * 256] = gv[j];");
+    // every coherent load is issued before the first is consumed (one round trip, not GP/256):
+    // 16-byte loads when a chunk's group partials are 16-byte aligned runs
+    if ((REP * PSZ) % 4 == 0 && (NH * PSZ) % 4 == 0 && part_off % 16 == 0) {
+        const int64_t Q4 = REP * PSZ / 4;                     // float4 per chunk
+        const int64_t PER = (NCH * Q4 + 255) / 256;
+        k.line("const float* gbase = a.scratch + " + std::to_string(part_off / 4) + " + grp * " + std::to_string(REP * PSZ) + ";");
+        k.line("sanic_f32x4 gv[" + std::to_string(PER) + "];");
+        k.line("#pragma unroll");
+        k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j) {");
+        k.line("  const int i = tid + j * 256;");
+        k.line("  const int ch = i / " + std::to_string(Q4) + ", w = i % " + std::to_string(Q4) + ";");
+        k.line("  gv[j] = sanic_ld4(gbase, (unsigned)((i < " + std::to_string(NCH * Q4) + " ? ch * " + std::to_string(NH * PSZ) + " + w * 4 : 0) * 4));");
+        k.line("}");
+        k.line("#pragma unroll");
+        k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j)");
+        k.line("  if (tid + j * 256 < " + std::to_string(NCH * Q4) + ") *(sanic_f32x4*)(g_lds + (tid + j * 256) * 4) = gv[j];");
+    } else {
+        const int64_t PER = (GP + 255) / 256;
+        k.line("float gv[" + std::to_string(PER) + "];");
+        k.line("#pragma unroll");
+        k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j) {");
+        k.line("  const int i = tid + j * 256;");
+        k.line("  const int ch = i / " + std::to_string(REP * PSZ) + ", rem = i % " + std::to_string(REP * PSZ) + ";");
+        k.line("  gv[j] = i < " + std::to_string(GP) + " ? sanic_ld(a.scratch + " + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " +
+               std::to_string(REP) + ") * " + std::to_string(PSZ) + " + rem) : 0.0f;");
+        k.line("}");
+        k.line("#pragma unroll");
+        k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j)");
+        k.line("  if (tid + j * 256 < " + std::to_string(GP) + ") g_lds[tid + j * 256] = gv[j];");
+    }
     k.line("__syncthreads();");
     k.line("if (tid == 0) sanic_st(cnt, 0u);");
     // per head (one wave each): M and the chunk weights

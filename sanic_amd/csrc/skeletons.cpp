@@ -697,8 +697,9 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         const int NSEG = (int)group.size();
         int RBI = K >= 8192 ? 4 : 2;
         if (const char* e = getenv("SANIC_GEMV_RB")) RBI = std::max(1, std::min(8, atoi(e)));
-        if (paired >= 0) RBI = 1;
-        const int RB = paired >= 0 ? NSEG : RBI;                 // rows per workgroup
+        if (paired >= 0) RBI = 2;
+        if (paired >= 0) if (const char* e = getenv("SANIC_GEMV_PRB")) RBI = std::max(1, std::min(4, atoi(e)));
+        const int RB = paired >= 0 ? RBI * NSEG : RBI;           // rows per workgroup
         const int64_t UNITS = paired >= 0 ? P0.N : NTOT;
         const int64_t nblocks = (UNITS + RBI - 1) / RBI;
         const int RW = RB * SC + SR;                             // partials per wave
@@ -711,12 +712,15 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         for (int q = 0; q < RB; q++) {
             std::string qs = std::to_string(q);
             if (paired >= 0) {
-                k.line("const idx_t row" + qs + " = (idx_t)blockIdx.x + " + std::to_string(q * P0.N) + ";");
-                k.line("const bool live" + qs + " = (idx_t)blockIdx.x < " + std::to_string(P0.N) + ";");
-                k.line("const int seg" + qs + " = " + qs + ";");
-                k.line("const idx_t nn" + qs + " = live" + qs + " ? (idx_t)blockIdx.x : 0;");
+                // row q = unit q / NSEG of this workgroup, segment q % NSEG
+                const int u = q / NSEG, g = q % NSEG;
+                const std::string unit = "((idx_t)blockIdx.x * " + std::to_string(RBI) + " + " + std::to_string(u) + ")";
+                k.line("const idx_t row" + qs + " = " + unit + " + " + std::to_string(g * P0.N) + ";");
+                k.line("const bool live" + qs + " = " + unit + " < " + std::to_string(P0.N) + ";");
+                k.line("const int seg" + qs + " = " + std::to_string(g) + ";");
+                k.line("const idx_t nn" + qs + " = live" + qs + " ? " + unit + " : 0;");
                 for (size_t b = 0; b < wb0.size(); b++)
-                    k.line("const " + std::string(ctype_of(wd0[b])) + "* __restrict__ wb" + std::to_string(b) + "_" + qs + " = " + R.param(seg_wbufs[q][b]) + ";");
+                    k.line("const " + std::string(ctype_of(wd0[b])) + "* __restrict__ wb" + std::to_string(b) + "_" + qs + " = " + R.param(seg_wbufs[g][b]) + ";");
                 continue;
             }
             k.line("const idx_t row" + qs + " = (idx_t)blockIdx.x * " + std::to_string(RBI) + " + " + qs + ";");
@@ -835,22 +839,24 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
             R.memo.pop_back();
             return v;
         };
-        if (paired >= 0) {
-            k.line("if (t == 0 && live0) {");
+        if (paired >= 0) for (int u = 0; u < RBI; u++) {
+            const std::string q0s = std::to_string(u * NSEG);
+            k.line("if (t == " + std::to_string(u) + " && live" + q0s + ") {");
             k.indent++;
-            k.line("const idx_t wi = nn0;");
+            k.line("const idx_t wi = nn" + q0s + ";");
             const sanic_stage& pst = d->stages[paired];
             std::map<int, std::string> outv;
-            for (int q = 0; q < RB; q++) {
-                std::string qs = std::to_string(q);
-                k.line("float pv" + qs + ";");
+            for (int g = 0; g < NSEG; g++) {
+                const int q = u * NSEG + g;
+                std::string gs = std::to_string(g);
+                k.line("float pv" + gs + ";");
                 k.line("{");
                 k.indent++;
-                std::string v = finish_row(k, q, q);
-                k.line("pv" + qs + " = " + v + ";");
+                std::string v = finish_row(k, q, g);
+                k.line("pv" + gs + " = " + v + ";");
                 k.indent--;
                 k.line("}");
-                outv[d->stages[group[q].stage].out_buffer] = "pv" + qs;
+                outv[d->stages[group[g].stage].out_buffer] = "pv" + gs;
             }
             std::vector<int> stack{pst.value};
             while (!stack.empty()) {
