@@ -327,6 +327,8 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     std::ostringstream src;
     src << kPrelude;
     src << "typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;\n";
+    src << "typedef short sanic_s16x4 __attribute__((ext_vector_type(4)));\n";
+    src << "typedef short sanic_s16x8 __attribute__((ext_vector_type(8)));\n";
     src << "typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;\n";
     src << R.args_struct({});
     src << "typedef __bf16 sanic_bf16x2 __attribute__((ext_vector_type(2)));\n";
@@ -397,7 +399,9 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("#pragma unroll");
     k.line("for (int dt = 0; dt < 4; ++dt) { o[dt][0] = (f32x4){0, 0, 0, 0}; o[dt][1] = (f32x4){0, 0, 0, 0}; }");
     k.line("float m_run[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};");
-    k.line("float l_run[2] = {0.0f, 0.0f};");
+    // row sums ℓ accumulate on the matrix cores: a row of ones times P^T (same bf16 P as O)
+    k.line("f32x4 lsum[2] = {(f32x4){0, 0, 0, 0}, (f32x4){0, 0, 0, 0}};");
+    k.line("const bf16x8 ones = {0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80};");
     const double LOG2E = 1.4426950408889634;
     // cooperative tile loads: K tile (64 keys × 64 d) and V tile, 2 × 16 B per thread each
     std::string kbase = std::to_string(P.kacc.addr.c0) + " + " + hterm(kc, kh, khc);
@@ -421,13 +425,8 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         c2.line("  const int ch = tid + u * 256;");
         c2.line("  const int r = ch >> 3, c8 = (ch & 7) * 8;");
         c2.line("  *(sanic_u32x4*)(&k_lds[" + buf + "][r * " + std::to_string(KS) + " + c8]) = kreg[u];");
-        if (v_rows) {
-            // transpose into V^T[e][key]
-            c2.line("  #pragma unroll");
-            c2.line("  for (int j = 0; j < 8; ++j) v_lds[" + buf + "][(c8 + j) * " + std::to_string(VS) + " + r] = (unsigned short)(vreg[u][j >> 1] >> (16 * (j & 1)));");
-        } else {
-            c2.line("  *(sanic_u32x4*)(&v_lds[" + buf + "][r * " + std::to_string(VS) + " + c8]) = vreg[u];");
-        }
+        // V rows ([key][e]) or V^T rows ([e][key]) as they lie in memory
+        c2.line("  *(sanic_u32x4*)(&v_lds[" + buf + "][r * " + std::to_string(VS) + " + c8]) = vreg[u];");
         c2.line("}");
     };
     k.line("if (klo < khi) {");
@@ -526,13 +525,11 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("}");
     k.indent--;
     k.line("}");
-    k.line("float ps = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));");
-    k.line("ps += ((p[8] + p[9]) + (p[10] + p[11])) + ((p[12] + p[13]) + (p[14] + p[15]));");
-    k.line("l_run[qt] = l_run[qt] * alpha + ps;");
     k.line("m_run[qt] = mn;");
     k.line("if (!__all(alpha == 1.0f)) {");   // the running max moved for some row: rescale
     k.line("  #pragma unroll");
     k.line("  for (int dt = 0; dt < 4; ++dt) { o[dt][qt][0] *= alpha; o[dt][qt][1] *= alpha; o[dt][qt][2] *= alpha; o[dt][qt][3] *= alpha; }");
+    k.line("  lsum[qt] *= alpha;");
     k.line("}");
     // P^T as the B operand for key step ks: slots 0..3 = keys 32ks + lq·4 + r (tile 2ks),
     // slots 4..7 = keys 32ks + 16 + lq·4 + r (tile 2ks+1); two slots per dword, RNE in hardware
@@ -550,14 +547,27 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("for (int qt = 0; qt < 2; ++qt) { pf[qt][0] = __builtin_bit_cast(bf16x8, pw[qt][0]); pf[qt][1] = __builtin_bit_cast(bf16x8, pw[qt][1]); }");
     // O^T += V^T · P^T ; V^T A operand: row e = dt·16 + l16, keys in the same slot order
     k.line("#pragma unroll");
+    k.line("for (int ks = 0; ks < 2; ++ks) {");
+    k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[0][ks], lsum[0], 0, 0, 0);");
+    k.line("  lsum[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[1][ks], lsum[1], 0, 0, 0);");
+    k.line("}");
+    k.line("#pragma unroll");
     k.line("for (int dt = 0; dt < 4; ++dt)");
     k.line("  #pragma unroll");
     k.line("  for (int ks = 0; ks < 2; ++ks) {");
-    k.line("    const unsigned short* vr = &v_lds[buf][(dt * 16 + l16) * " + std::to_string(VS) + " + ks * 32 + lq * 4];");
-    k.line("    const uint2 lo4 = *(const uint2*)(vr), hi4 = *(const uint2*)(vr + 16);");
-    k.line("    bf16x8 va;");
-    k.line("    va[0] = (short)(lo4.x & 0xFFFF); va[1] = (short)(lo4.x >> 16); va[2] = (short)(lo4.y & 0xFFFF); va[3] = (short)(lo4.y >> 16);");
-    k.line("    va[4] = (short)(hi4.x & 0xFFFF); va[5] = (short)(hi4.x >> 16); va[6] = (short)(hi4.y & 0xFFFF); va[7] = (short)(hi4.y >> 16);");
+    if (v_rows) {
+        // V rows in LDS, read transposed (ds_read_b64_tr_b16): in each 16-lane group, source
+        // lane s reads 4 values of e at key row (base + s/4), e = dt·16 + 4·(s%4); lane i then
+        // holds keys base + 0..3 of e = dt·16 + i — slots 0..3, and base + 16 gives slots 4..7
+        k.line("    const unsigned short* vr = &v_lds[buf][(ks * 32 + lq * 4 + (l16 >> 2)) * " + std::to_string(VS) + " + dt * 16 + (l16 & 3) * 4];");
+        k.line("    const sanic_s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(vr));");
+        k.line("    const sanic_s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(vr + 16 * " + std::to_string(VS) + "));");
+        k.line("    const bf16x8 va = __builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));");
+    } else {
+        k.line("    const unsigned short* vr = &v_lds[buf][(dt * 16 + l16) * " + std::to_string(VS) + " + ks * 32 + lq * 4];");
+        k.line("    const uint2 lo4 = *(const uint2*)(vr), hi4 = *(const uint2*)(vr + 16);");
+        k.line("    const bf16x8 va = __builtin_bit_cast(bf16x8, (sanic_u32x4){lo4.x, lo4.y, hi4.x, hi4.y});");
+    }
     k.line("    o[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[0][ks], o[dt][0], 0, 0, 0);");
     k.line("    o[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[1][ks], o[dt][1], 0, 0, 0);");
     k.line("  }");
@@ -578,8 +588,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("#pragma unroll");
     k.line("for (int qt = 0; qt < 2; ++qt) {");
     k.indent++;
-    k.line("float lt = l_run[qt];");
-    k.line("lt = wave_sum_x4(lt);");
+    k.line("const float lt = lsum[qt][0];");
     k.line("const idx_t qi = q0 + qt * 16 + l16;");
     k.line("#pragma unroll");
     k.line("for (int dt = 0; dt < 4; ++dt)");
