@@ -23,6 +23,8 @@
 #include <algorithm>
 #include <cmath>
 
+#include <functional>
+
 #include "emit.h"
 #include "skeletons.h"
 
@@ -337,11 +339,17 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
            "  return __builtin_bit_cast(unsigned, __builtin_convertvector((sanic_f32x2){x, y}, sanic_bf16x2));\n}\n";
     // max across the 4 lane groups of a query column (lanes l, l^16, l^32, l^48): gfx950
     // permlane swaps, no LDS round trip
+    // raw hardware max (scores from the matrix cores never carry signaling NaNs, so the
+    // operand quieting fmaxf adds in IEEE mode is pure overhead here)
+    src << "__device__ __forceinline__ float hmax(float a, float b) {\n"
+           "  float r; asm(\"v_max_f32 %0, %1, %2\" : \"=v\"(r) : \"v\"(a), \"v\"(b)); return r;\n}\n";
+    src << "__device__ __forceinline__ float hmax3(float a, float b, float c) {\n"
+           "  float r; asm(\"v_max3_f32 %0, %1, %2, %3\" : \"=v\"(r) : \"v\"(a), \"v\"(b), \"v\"(c)); return r;\n}\n";
     src << "__device__ __forceinline__ float wave_max_x4(float v) {\n"
            "  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);\n"
-           "  v = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));\n"
+           "  v = hmax(__uint_as_float(r32[0]), __uint_as_float(r32[1]));\n"
            "  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);\n"
-           "  return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));\n}\n";
+           "  return hmax(__uint_as_float(r16[0]), __uint_as_float(r16[1]));\n}\n";
     src << "__device__ __forceinline__ float wave_sum_x4(float v) {\n"
            "  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);\n"
            "  v = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);\n"
@@ -403,6 +411,19 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("f32x4 lsum[2] = {(f32x4){0, 0, 0, 0}, (f32x4){0, 0, 0, 0}};");
     k.line("const bf16x8 ones = {0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80};");
     const double LOG2E = 1.4426950408889634;
+    // Lazy reference max: the running max moves only when a tile's max exceeds it by more than
+    // TAU (natural-log units, so every p stays below 2^8): the online softmax is exact for any
+    // reference point, and rescaling O and ℓ becomes rare. Only when the projection does not
+    // read the max slot itself.
+    std::function<bool(int)> reads_f = [&](int e) -> bool {
+        const sanic_expr& x = d->exprs[e];
+        if (x.op == SANIC_EX_F) return x.index == P.max_slot;
+        if (x.op >= SANIC_EX_CONST) return false;
+        for (int ch : {x.a, x.b, x.c}) if (ch >= 0 && reads_f(ch)) return true;
+        return false;
+    };
+    const bool lazy = !reads_f(c.project) && !getenv("SANIC_FLASH_EAGER");
+    const double TAU = 8.0 / LOG2E;
     // cooperative tile loads: K tile (64 keys × 64 d) and V tile, 2 × 16 B per thread each
     std::string kbase = std::to_string(P.kacc.addr.c0) + " + " + hterm(kc, kh, khc);
     std::string vbase = std::to_string(P.vacc.addr.c0) + " + " + hterm(vc, vh, vhc);
@@ -434,6 +455,10 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     load_tile(k, "klo");
     store_tile(k, "0");
     k.line("__syncthreads();");
+    // every load issued so far (the Q fragments, the first tile) has landed: without this the
+    // loop's first MFMA carries a conservative vmcnt wait that, in every later iteration, stalls
+    // on the next tile's prefetch
+    k.line("__builtin_amdgcn_s_waitcnt(0);");
     k.line("int buf = 0;");
     k.line("for (idx_t t0 = klo; t0 < khi; t0 += 64) {");
     k.indent++;
@@ -474,11 +499,13 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         // full tiles: score = dot·c, so max and exp2 work on the raw dot (c > 0)
         k.line("if (full) {");
         k.indent++;
-        k.line("float mt = fmaxf(fmaxf(s[0][qt][0], s[0][qt][1]), fmaxf(s[0][qt][2], s[0][qt][3]));");
-        k.line("#pragma unroll");
-        k.line("for (int kt = 1; kt < 4; ++kt) mt = fmaxf(mt, fmaxf(fmaxf(s[kt][qt][0], s[kt][qt][1]), fmaxf(s[kt][qt][2], s[kt][qt][3])));");
+        // 16 → 1 in 8 three-input maxes
+        k.line("const float ma = hmax3(s[0][qt][0], s[0][qt][1], s[0][qt][2]), mb_ = hmax3(s[0][qt][3], s[1][qt][0], s[1][qt][1]);");
+        k.line("const float mc = hmax3(s[1][qt][2], s[1][qt][3], s[2][qt][0]), md = hmax3(s[2][qt][1], s[2][qt][2], s[2][qt][3]);");
+        k.line("const float me = hmax3(s[3][qt][0], s[3][qt][1], s[3][qt][2]);");
+        k.line("float mt = hmax3(hmax3(ma, mb_, mc), hmax3(md, me, s[3][qt][3]), ma);");
         k.line("mt = wave_max_x4(mt) * " + flit(scale_c) + ";");
-        k.line("mn = fmaxf(m_run[qt], mt);");
+        k.line(lazy ? "mn = mt > m_run[qt] + " + flit(TAU) + " ? mt : m_run[qt];" : "mn = fmaxf(m_run[qt], mt);");
         k.line("alpha = m_run[qt] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - mn) * " + flit(LOG2E) + ");");
         k.line("if (__all(mn > -1e29f)) {");
         k.line("  const float mb = mn * " + flit(LOG2E) + ";");
@@ -509,7 +536,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("#pragma unroll");
     k.line("for (int i = 4; i < 16; i += 2) mt = fmaxf(mt, fmaxf(sv[i], sv[i + 1]));");
     k.line("mt = wave_max_x4(mt);");
-    k.line("mn = fmaxf(m_run[qt], mt);");
+    k.line(lazy ? "mn = mt > m_run[qt] + " + flit(TAU) + " ? mt : m_run[qt];" : "mn = fmaxf(m_run[qt], mt);");
     // the carrier's guarded rescale: a side whose max is −∞ weighs 0
     k.line("alpha = m_run[qt] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - mn) * " + flit(LOG2E) + ");");
     // Fast form exp2(s·log2e − m·log2e) (one FMA) while every row of the wave has a moderate
