@@ -350,17 +350,18 @@ struct GemvPlan {
     std::vector<int> cslots, rslots;
 };
 
-static std::vector<Sym> weight_coords(const sanic_program_desc* d, const sanic_stage& st, int w, int ndim) {
+// weight leaf coordinates over {0: n, 1: k} (swapped: {0: k, 1: n}, runs of 8 along n)
+static std::vector<Sym> weight_coords(const sanic_program_desc* d, const sanic_stage& st, int w, int ndim, bool swapped = false) {
     const sanic_node& wn = d->nodes[st.leaf[w]];
     std::vector<Sym> cw(wn.rank);
     for (int j = 0; j < wn.rank; j++) {
         int b = st.bind[w][j];
-        cw[j] = b == SANIC_BIND_STREAM ? Sym::var(1) : b == ndim ? Sym::var(0) : Sym();
+        cw[j] = b == SANIC_BIND_STREAM ? Sym::var(swapped ? 0 : 1) : b == ndim ? Sym::var(swapped ? 1 : 0) : Sym();
     }
     return cw;
 }
 
-static bool gemv_plan(const sanic_program_desc* d, int si, GemvPlan& P) {
+static bool gemv_plan(const sanic_program_desc* d, int si, GemvPlan& P, bool kmajor = false) {
     const sanic_stage& st = d->stages[si];
     if (st.kind != SANIC_STAGE_FUSED) return false;
     const sanic_carrier& c = st.carrier;
@@ -404,6 +405,11 @@ static bool gemv_plan(const sanic_program_desc* d, int si, GemvPlan& P) {
     if (P.cslots.empty() || P.cslots.size() > 2) return false;
     VecW vw{d};
     Code lc, dc;
+    if (kmajor) {
+        // N-contiguous weights ([in, out]): runs of 8 along n
+        vw.render(lc, dc, st.leaf[w], weight_coords(d, st, w, ndim, true), {P.K, P.N});
+        return vw.ok && vw.contiguous;
+    }
     vw.render(lc, dc, st.leaf[w], weight_coords(d, st, w, ndim), {P.N, P.K});
     // K-contiguous weights (the reference's [out, in] layout): every access moves by 1 or 0
     // along a run of k; other layouts go to the generic fold
@@ -1190,7 +1196,167 @@ bool lower_pointwise_skeleton(const sanic_program_desc* d, int si, int64_t&, Low
     return true;
 }
 
+// ───────────────────────── gemv over N-contiguous weights ──────────────────────────────────
+// y[n] = project(Σ_k into(x(k), W[k, n])) with W stored [K, N] (the K-major layout of the
+// RMSNorm-fused projection's configuration): each lane owns 8 adjacent columns (one 16-byte
+// load per k row), a workgroup covers 512 columns × a K slice whose rows its 4 waves split,
+// the waves meet in LDS, and the workgroups of a column group meet through f32 partials in
+// scratch: the last one to arrive adds the K slices in order, folds the row slots (Σx², …)
+// over the whole of K itself, projects, runs the epilogue and stores.
+bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
+    GemvPlan P;
+    if (getenv("SANIC_HIP_GENERIC") || !gemv_plan(d, si, P, true)) return false;
+    const sanic_stage& st = d->stages[si];
+    const sanic_carrier& c = st.carrier;
+    const int64_t N = P.N, K = P.K;
+    if (N % 512 || K % 64) return false;
+    const int SC = (int)P.cslots.size(), SR = (int)P.rslots.size();
+    const int64_t NCG = N / 512;
+    int64_t KS = std::max<int64_t>(1, std::min<int64_t>(K / 128, 128 / NCG));   // K slices
+    if (const char* e = getenv("SANIC_GEMVT_KS")) KS = std::max<int64_t>(1, atoi(e));
+    while (K % KS || (K / KS) % 4) KS--;
+    const int64_t KB = K / KS, KW = KB / 4;                                    // rows per slice / wave
+    int64_t part_off = scratch;
+    scratch += ((KS * SC * N * 4 + 255) / 256) * 256;
+    int64_t rpart_off = scratch;                 // per-slice row-slot partials [NCG][KS][SR]
+    scratch += ((NCG * KS * std::max(SR, 1) * 4 + 255) / 256) * 256;
+    int64_t counter_off = scratch;
+    scratch += ((NCG * 4 + 255) / 256) * 256;
+
+    Renderer R(d);
+    Code k;
+    k.indent = 1;
+    k.line("__shared__ __attribute__((aligned(16))) float red[4][" + std::to_string(SC * 512) + "];");
+    k.line("const int t = threadIdx.x, lane = t & 63, wv = t >> 6;");
+    k.line("const idx_t cg = blockIdx.x % " + std::to_string(NCG) + ", ks = blockIdx.x / " + std::to_string(NCG) + ";");
+    k.line("const idx_t n0 = cg * 512 + lane * 8;");
+    k.line("const idx_t kbeg = ks * " + std::to_string(KB) + " + wv * " + std::to_string(KW) + ";");
+    for (size_t b = 0; b < 1; b++) {}
+    // weight runs: one per k row of this wave
+    std::vector<std::vector<std::string>> wv_(KW);
+    Code wdc;
+    wdc.indent = k.indent;
+    std::vector<int> wbufs, wdts;
+    for (int64_t i = 0; i < KW; i++) {
+        VecW vw{d};
+        vw.nn = "(kbeg + " + std::to_string(i) + ")";
+        vw.k0 = "n0";
+        vw.ptr = "wb";
+        vw.psfx = "";
+        vw.sfx = "_" + std::to_string(i);
+        Code l1;
+        l1.indent = k.indent;
+        wv_[i] = vw.render(l1, wdc, st.leaf[P.w], weight_coords(d, st, P.w, P.ndim, true), {K, N});
+        if (!vw.ok) return false;
+        if (i == 0) {
+            wbufs = vw.bufs;
+            wdts = vw.dtypes;
+            for (size_t b = 0; b < wbufs.size(); b++)
+                k.line("const " + std::string(ctype_of(wdts[b])) + "* __restrict__ wb" + std::to_string(b) + " = " + R.param(wbufs[b]) + ";");
+        }
+        k.s << l1.str();
+    }
+    k.s << wdc.str();
+    // activation factors per k row (the same for every lane: broadcast loads)
+    for (int cs = 0; cs < SC; cs++)
+        for (int j = 0; j < 8; j++) k.line("float acc" + std::to_string(cs) + "_" + std::to_string(j) + " = 0.0f;");
+    for (int r = 0; r < SR; r++) k.line("float rpart" + std::to_string(r) + " = 0.0f;");
+    for (int64_t i = 0; i < KW; i++) {
+        k.line("{");
+        k.indent++;
+        k.line("const idx_t kr = kbeg + " + std::to_string(i) + ";");
+        R.memo.emplace_back();
+        for (int l = 0; l < st.n_leaves; l++) {
+            if (l == P.w) continue;
+            const sanic_node& ln = d->nodes[st.leaf[l]];
+            std::vector<std::string> lc(ln.rank);
+            for (int j = 0; j < ln.rank; j++) lc[j] = st.bind[l][j] == SANIC_BIND_STREAM ? "kr" : "0";
+            k.line("const float x" + std::to_string(l) + " = " + R.value(k, st.leaf[l], lc) + ";");
+        }
+        for (int cs = 0; cs < SC; cs++) {
+            std::string f = expr_without(R, k, c.into[P.cslots[cs]], P.w, "x");
+            for (int j = 0; j < 8; j++) {
+                std::string a = "acc" + std::to_string(cs) + "_" + std::to_string(j);
+                k.line(a + " = fmaf(" + f + ", " + wv_[i][j] + ", " + a + ");");
+            }
+        }
+        // row slots of this wave's rows (every lane holds the same value)
+        for (int r = 0; r < SR; r++) k.line("rpart" + std::to_string(r) + " += " + R.expr(k, c.into[P.rslots[r]], "x", "", "", "") + ";");
+        R.memo.pop_back();
+        k.indent--;
+        k.line("}");
+    }
+    // waves -> LDS -> this slice's partial for 512 columns
+    for (int cs = 0; cs < SC; cs++) {
+        std::string css = std::to_string(cs);
+        k.line("*(sanic_f32x4*)(&red[wv][" + css + " * 512 + lane * 8]) = (sanic_f32x4){acc" + css + "_0, acc" + css + "_1, acc" + css + "_2, acc" + css + "_3};");
+        k.line("*(sanic_f32x4*)(&red[wv][" + css + " * 512 + lane * 8 + 4]) = (sanic_f32x4){acc" + css + "_4, acc" + css + "_5, acc" + css + "_6, acc" + css + "_7};");
+    }
+    if (SR > 0) {
+        k.line("__shared__ float rred[4][" + std::to_string(SR) + "];");
+        for (int r = 0; r < SR; r++) k.line("if (lane == 0) rred[wv][" + std::to_string(r) + "] = rpart" + std::to_string(r) + ";");
+    }
+    k.line("__syncthreads();");
+    for (int r = 0; r < SR; r++) {
+        std::string rs = std::to_string(r);
+        k.line("if (t == 0) sanic_st(a.scratch + " + std::to_string(rpart_off / 4) + " + (cg * " + std::to_string(KS) + " + ks) * " + std::to_string(SR) + " + " + rs +
+               ", ((rred[0][" + rs + "] + rred[1][" + rs + "]) + rred[2][" + rs + "]) + rred[3][" + rs + "]);");
+    }
+    k.line("for (int i = t; i < " + std::to_string(SC * 512) + "; i += 256) {");
+    k.line("  const float v = ((red[0][i] + red[1][i]) + red[2][i]) + red[3][i];");
+    k.line("  const int cs = i / 512, col = i % 512;");
+    k.line("  sanic_st(a.scratch + " + std::to_string(part_off / 4) + " + (ks * " + std::to_string(SC) + " + cs) * " + std::to_string(N) + " + cg * 512 + col, v);");
+    k.line("}");
+    k.line("__shared__ int sanic_last;");
+    k.line("__builtin_amdgcn_s_waitcnt(0);");
+    k.line("__syncthreads();");
+    k.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(counter_off) + ") + cg;");
+    k.line("if (t == 0) sanic_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == " + std::to_string(KS) + "u - 1u;");
+    k.line("__syncthreads();");
+    k.line("if (!sanic_last) return;");
+    k.line("if (t == 0) sanic_st(cnt, 0u);");
+    // row slots: the K slices' partials, in slice order
+    for (int r = 0; r < SR; r++) {
+        std::string rs = std::to_string(r);
+        k.line("float racc" + rs + " = 0.0f;");
+        k.line("#pragma unroll");
+        k.line("for (int q = 0; q < " + std::to_string(KS) + "; ++q) racc" + rs + " += sanic_ld(a.scratch + " + std::to_string(rpart_off / 4) + " + (cg * " +
+               std::to_string(KS) + " + q) * " + std::to_string(SR) + " + " + rs + ");");
+    }
+    // the K slices of each column, in slice order; then project / epilogue / store
+    k.line("for (int col = t; col < 512; col += 256) {");
+    k.indent++;
+    k.line("const idx_t nn = cg * 512 + col;");
+    std::string arr = "float accq[" + std::to_string(SC) + "] = {";
+    for (int cs = 0; cs < SC; cs++) arr += cs ? ", 0.0f" : "0.0f";
+    k.line(arr + "};");
+    k.line("float pv[" + std::to_string(KS * SC) + "];");
+    k.line("#pragma unroll");
+    k.line("for (int q = 0; q < " + std::to_string(KS * SC) + "; ++q) pv[q] = sanic_ld(a.scratch + " + std::to_string(part_off / 4) + " + (idx_t)q * " + std::to_string(N) + " + nn);");
+    k.line("#pragma unroll");
+    k.line("for (int q = 0; q < " + std::to_string(KS) + "; ++q)");
+    k.line("  #pragma unroll");
+    k.line("  for (int cs = 0; cs < " + std::to_string(SC) + "; ++cs) accq[cs] += pv[q * " + std::to_string(SC) + " + cs];");
+    R.memo.emplace_back();
+    gemv_finish(R, k, d, P, false);
+    R.memo.pop_back();
+    k.indent--;
+    k.line("}");
+
+    const std::string kname = "sanic_gemvt_" + std::to_string(N) + "x" + std::to_string(K);
+    std::ostringstream src;
+    src << kPrelude << R.args_struct({"float* __restrict__ scratch"})
+        << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
+    out.kernel_kind = "skeleton:gemv_kmajor[" + std::to_string(KS) + " slices]";
+    out.source = src.str();
+    std::vector<Arg> args = R.arg_list();
+    args.push_back({Arg::SCRATCH, 0});
+    out.launches.push_back({kname, "", dim3((unsigned)(NCG * KS)), dim3(256), 0, args});
+    return true;
+}
+
 bool lower_skeleton(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
+    if (lower_gemv_kmajor(d, si, scratch, out)) return true;
     if (lower_gemm(d, si, scratch, out)) return true;
     if (lower_flash_prefill(d, si, scratch, out)) return true;
     if (lower_attn_decode(d, si, scratch, out)) return true;

@@ -49,7 +49,7 @@ def test_lowering_chooses_the_expected_kernel(name):
         "A": (configs.direct_attention(), 0, "fold:scalar"),
         "A_coop": (configs.direct_attention(sched=Sched(lane_stream=True, waves=2)), 0, "fold:coop"),
         "A_split": (configs.direct_attention(sched=Sched(lane_stream=True, waves=2, split=4)), 0, "fold:split"),
-        "B1": (configs.rmsnorm_projection(kmajor=True), 0, ""),
+        "B1": (configs.rmsnorm_projection(kmajor=True), 0, "skeleton:gemv_kmajor"),
         "B1_rows": (configs.rmsnorm_projection(kmajor=False), 0, "skeleton:gemv"),
         "D1": (configs.int4_matmul(), 0, "skeleton:gemv"),
         "C3": (configs.decode_attention(), 0, "skeleton:attn_decode"),

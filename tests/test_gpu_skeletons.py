@@ -38,6 +38,21 @@ def test_b1_rmsnorm_gemv_rows_layout(dev, M):
     assert bf16_rel(got["y"], want) < 2e-2
 
 
+@pytest.mark.parametrize("K,N", [(2048, 8192), (256, 1024)])
+def test_b1_rmsnorm_gemv_kmajor(dev, K, N):
+    """Config B1 as configured: W bf16 [K, N] (K-major), the N-contiguous gemv skeleton."""
+    prog = configs.rmsnorm_projection(M=1, K=K, N=N, kmajor=True)
+    x = _bf16_vals(111, K).reshape(1, K)
+    g = _bf16_vals(112, K, 1.0, 0.02)
+    wbits = oracle.synth_bf16(113, K * N, "normal", 0.0, 0.02).reshape(K, N)
+    w = from_bf16_bits(wbits).astype(np.float64)
+    got, exe = run_on_gpu(dev, prog, {"x": x, "g": g, "W": w})
+    want = oracle.rmsnorm_proj(x, g, wbits, 1e-5)
+    print(exe.stage_kernel(0), bf16_rel(got["y"], want))
+    assert exe.stage_kernel(0).startswith("skeleton:gemv_kmajor")
+    assert bf16_rel(got["y"], want) < 2e-2
+
+
 def test_d1_int4_gemv(dev):
     """Config D1: packed uint4 [8192, 2048], group 64, s ~ U(0.001, 0.02), z = 8·s."""
     M, K, N, G = 1, 2048, 8192, 64
