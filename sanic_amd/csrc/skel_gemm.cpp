@@ -94,6 +94,15 @@ bool gemm_plan(const sanic_program_desc* d, int si, GemmPlan& P) {
     }
     // the weight is the one dim-bound leaf that every row slot ignores and every other slot
     // multiplies in exactly once; all other dim-bound leaves share the other (row) dim
+    // Of the valid role assignments, prefer the one that recomputes the least: a side that is not
+    // a stored bf16 value (x·g, a dequantized weight) is rebuilt by every workgroup along the
+    // other output dim.
+    GemmPlan best;
+    int64_t best_cost = -1;
+    auto raw_leaf = [&](int l) {
+        const sanic_node& n = d->nodes[st.leaf[l]];
+        return n.kind == SANIC_NODE_INPUT && n.dtype == SANIC_BF16;
+    };
     for (auto& cand : dimmed) {
         GemmPlan Q = P;
         Q.w = cand.first;
@@ -112,8 +121,27 @@ bool gemm_plan(const sanic_program_desc* d, int si, GemmPlan& P) {
             else if (linear_mul(d, c.into[k], Q.w)) Q.cslots.push_back(k);
             else good = false;
         }
-        if (good && Q.cslots.size() == 1) { P = Q; break; }
+        if (!good || Q.cslots.size() != 1) continue;
+        bool a_raw = false;
+        {
+            const sanic_expr& e = d->exprs[c.into[Q.cslots[0]]];
+            if (e.op == SANIC_OP_MUL) {
+                const sanic_expr& ea = d->exprs[e.a];
+                const sanic_expr& eb = d->exprs[e.b];
+                const sanic_expr* other = nullptr;
+                if (ea.op == SANIC_EX_ITEM && ea.index == Q.w) other = &eb;
+                if (eb.op == SANIC_EX_ITEM && eb.index == Q.w) other = &ea;
+                if (other && other->op == SANIC_EX_ITEM && raw_leaf(other->index)) a_raw = true;
+            }
+        }
+        // element rebuilds: A (M×K) once per column block, B (N×K) once per row block
+        const int64_t Mq = st.grid[Q.mdim], Nq = st.grid[Q.ndim];
+        const int64_t cost = (a_raw ? 0 : Mq * ((Nq + 127) / 128)) + (raw_leaf(Q.w) ? 0 : Nq * ((Mq + 127) / 128));
+        // ties: keep the stored bf16 operand on the A side (its tile needs no arithmetic)
+        const int64_t key = cost * 2 + (a_raw ? 0 : 1);
+        if (best_cost < 0 || key < best_cost) { best = Q; best_cost = key; }
     }
+    P = best;
     if (P.w < 0) return false;
     P.M = st.grid[P.mdim];
     P.N = st.grid[P.ndim];
@@ -183,6 +211,23 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         render_weight_run(d, st.leaf[P.w], cw, {N, K}, l1, d1, "nn", "k0", "_p", wbufs, wdts, ok, contig, raw, false);
         if (!ok) return false;
     }
+    // N-contiguous weights ([K, N]): runs of 8 along n, the B tile kept [k][n] in LDS and read
+    // transposed into the MFMA's k-major operand (ds_read_b64_tr_b16)
+    std::vector<Sym> cwt(wn.rank);
+    for (int j = 0; j < wn.rank; j++) {
+        int b = st.bind[P.w][j];
+        cwt[j] = b == SANIC_BIND_STREAM ? Sym::var(0) : b == P.ndim ? Sym::var(1) : Sym();
+    }
+    bool bkn = false;
+    if (!contig && !getenv("SANIC_GEMM_NO_TR")) {
+        std::vector<int> tb, td;
+        bool tok = true, tc = true;
+        std::string tr;
+        Code l1, d1;
+        render_weight_run(d, st.leaf[P.w], cwt, {K, N}, l1, d1, "kk", "n0", "_p", tb, td, tok, tc, tr, false);
+        bkn = tok && tc;
+    }
+    const int BNS = BN + 8;                   // [k][n] B tile row stride (bf16)
     // row leaves vector forms over vars {0: m, 1: k}
     std::vector<std::vector<Sym>> crow;
     for (int l : P.rows) {
@@ -204,9 +249,10 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     Code k;
     k.indent = 1;
     k.line("__shared__ unsigned short a_lds[2][" + std::to_string(BM * AS) + "];");
-    k.line("__shared__ unsigned short b_lds[2][" + std::to_string(BN * BS) + "];");
+    const int BTILE = bkn ? 64 * BNS : BN * BS;
+    k.line("__shared__ unsigned short b_lds[2][" + std::to_string(BTILE) + "];");
     if (splitA) k.line("__shared__ unsigned short a_lo[2][" + std::to_string(BM * AS) + "];");
-    if (splitB) k.line("__shared__ unsigned short b_lo[2][" + std::to_string(BN * BS) + "];");
+    if (splitB) k.line("__shared__ unsigned short b_lo[2][" + std::to_string(BTILE) + "];");
     if (SR) k.line("__shared__ float rs_lds[" + std::to_string(BM * SR) + "];");
     k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
     k.line("const int l16 = lane & 15, lq = lane >> 4;");
@@ -251,7 +297,12 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         for (int r = 0; r < RUNS_B; r++) {
             std::string rs = std::to_string(r);
             std::string nn, kk;
-            if (contig) {
+            if (bkn) {
+                // chunk c = tid + 256·r: k row c / (BN/8), 8 columns from (c % (BN/8))·8
+                const std::string cc = "(tid + " + std::to_string(r * 256) + ")";
+                kk = "(" + kt0 + " + " + cc + " / " + std::to_string(BN / 8) + ")";
+                nn = "(n0 + (" + cc + " % " + std::to_string(BN / 8) + ") * 8)";
+            } else if (contig) {
                 nn = "(n0 + (tid / 8) + " + std::to_string(r * 32) + ")";
                 kk = "(" + kt0 + " + (tid % 8) * 8)";
             } else {
@@ -263,7 +314,8 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             std::string rr;
             Code l1, d1;
             l1.indent = d1.indent = c2.indent;
-            auto vals = render_weight_run(d, st.leaf[P.w], cw, {N, K}, l1, d1, nn, kk, "_b" + rs + sfx, rb, rd, rok, rc, rr, false);
+            auto vals = bkn ? render_weight_run(d, st.leaf[P.w], cwt, {K, N}, l1, d1, kk, nn, "_b" + rs + sfx, rb, rd, rok, rc, rr, false)
+                            : render_weight_run(d, st.leaf[P.w], cw, {N, K}, l1, d1, nn, kk, "_b" + rs + sfx, rb, rd, rok, rc, rr, false);
             for (size_t b = 0; b < rb.size(); b++)
                 c2.line("const " + std::string(ctype_of(rd[b])) + "* __restrict__ wb" + std::to_string(b) + "_b" + rs + sfx + " = " + R.param(rb[b]) + ";");
             c2.s << l1.str();
@@ -322,15 +374,21 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         for (int r = 0; r < RUNS_B; r++) {
             std::string rs = std::to_string(r);
             std::string row, col;
-            if (contig) {
+            int stride = BS;
+            if (bkn) {
+                const std::string cc = "(tid + " + std::to_string(r * 256) + ")";
+                row = "(" + cc + " / " + std::to_string(BN / 8) + ")";
+                col = "((" + cc + " % " + std::to_string(BN / 8) + ") * 8)";
+                stride = BNS;
+            } else if (contig) {
                 row = "((tid / 8) + " + std::to_string(r * 32) + ")";
                 col = "((tid % 8) * 8)";
             } else {
                 row = "(tid % " + std::to_string(BN) + ")";
                 col = "(((tid / " + std::to_string(BN) + ") + " + std::to_string(r * (256 / BN)) + ") * 8)";
             }
-            c2.line("*(sanic_u32x4*)(&b_lds[" + buf + "][" + row + " * " + std::to_string(BS) + " + " + col + "]) = rb" + rs + sfx + ";");
-            if (splitB) c2.line("*(sanic_u32x4*)(&b_lo[" + buf + "][" + row + " * " + std::to_string(BS) + " + " + col + "]) = rl" + rs + sfx + ";");
+            c2.line("*(sanic_u32x4*)(&b_lds[" + buf + "][" + row + " * " + std::to_string(stride) + " + " + col + "]) = rb" + rs + sfx + ";");
+            if (splitB) c2.line("*(sanic_u32x4*)(&b_lo[" + buf + "][" + row + " * " + std::to_string(stride) + " + " + col + "]) = rl" + rs + sfx + ";");
         }
         c2.indent--;
         c2.line("}");
@@ -351,8 +409,24 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         c2.line("  }");
         c2.line("  #pragma unroll");
         c2.line("  for (int j = 0; j < " + NTs + "; ++j) {");
-        c2.line("    bf[j] = *(const bf16x8*)(&b_lds[" + buf + "]" + bidx + ");");
-        if (splitB) c2.line("    bfl[j] = *(const bf16x8*)(&b_lo[" + buf + "]" + bidx + ");");
+        if (bkn) {
+            // rows ks·32 + lq·8 + (0..3 | 4..7), column wn + j·16 + l16: in each 16-lane group,
+            // source lane s reads 4 columns 4·(s%4) of row base + s/4; lane i gets 4 rows of column i
+            const std::string br = "[(ks * 32 + lq * 8 + (l16 >> 2)) * " + std::to_string(BNS) + " + wn + j * 16 + (l16 & 3) * 4]";
+            auto tr = [&](const std::string& arr, const std::string& dst) {
+                c2.line("    {");
+                c2.line("      const unsigned short* bp = &" + arr + "[" + buf + "]" + br + ";");
+                c2.line("      const sanic_s16x4 t0_ = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(bp));");
+                c2.line("      const sanic_s16x4 t1_ = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(bp + 4 * " + std::to_string(BNS) + "));");
+                c2.line("      " + dst + " = __builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(t0_, t1_, 0, 1, 2, 3, 4, 5, 6, 7));");
+                c2.line("    }");
+            };
+            tr("b_lds", "bf[j]");
+            if (splitB) tr("b_lo", "bfl[j]");
+        } else {
+            c2.line("    bf[j] = *(const bf16x8*)(&b_lds[" + buf + "]" + bidx + ");");
+            if (splitB) c2.line("    bfl[j] = *(const bf16x8*)(&b_lo[" + buf + "]" + bidx + ");");
+        }
         c2.line("  }");
         c2.line("  #pragma unroll");
         c2.line("  for (int i = 0; i < " + MTs + "; ++i)");
@@ -432,6 +506,8 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     std::ostringstream src;
     src << kPrelude;
     src << "typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;\n";
+    src << "typedef short sanic_s16x4 __attribute__((ext_vector_type(4)));\n";
+    src << "typedef short sanic_s16x8 __attribute__((ext_vector_type(8)));\n";
     src << "typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;\n";
     src << "typedef __bf16 sanic_bf16x2 __attribute__((ext_vector_type(2)));\n";
     src << "typedef float sanic_f32x2 __attribute__((ext_vector_type(2)));\n";
@@ -443,7 +519,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
            "  lo = pk_bf16(x - __uint_as_float(h << 16), y - __uint_as_float(h & 0xFFFF0000u));\n}\n";
     src << R.args_struct({});
     src << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
-    out.kernel_kind = "skeleton:gemm[" + std::to_string(BM) + "x" + std::to_string(BN) + (splitA ? ",a2" : "") + (splitB ? ",b2" : "") + "]";
+    out.kernel_kind = "skeleton:gemm[" + std::to_string(BM) + "x" + std::to_string(BN) + (splitA ? ",a2" : "") + (splitB ? ",b2" : "") + (bkn ? ",kn" : "") + "]";
     out.source = src.str();
     out.launches.push_back({kname, "", dim3((unsigned)((M / BM) * (N / BN))), dim3(256), 0, R.arg_list()});
     return true;
