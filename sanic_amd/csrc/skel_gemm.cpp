@@ -160,7 +160,6 @@ std::vector<std::string> render_weight_run(const sanic_program_desc* d, int node
                                            bool stream);
 
 bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
-    (void)scratch;
     GemmPlan P;
     if (!gemm_plan(d, si, P)) return false;
     const sanic_stage& st = d->stages[si];
@@ -169,6 +168,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     const int BM = M % 128 == 0 ? 128 : 64;
     int BN = 128;
     while (BN > 32 && (M / BM) * (N / BN) < 256) BN /= 2;
+    if (const char* e = getenv("SANIC_GEMM_BN")) BN = std::max(32, std::min(128, atoi(e)));
     if (N % BN) return false;
     const int WM = BM / 2, WN = BN / 2;       // per-wave tile
     const int MT = WM / 16, NT = WN / 16;
@@ -246,6 +246,70 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         crow.push_back(cr);
     }
 
+    // A operands that need arithmetic (x·g of the fused RMSNorm) are built once by a first
+    // launch into bf16 hi/lo planes [M][K] (plus the row slots), instead of by every one of the
+    // N/BN column workgroups
+    const bool pre = splitA && N / BN >= 4 && K % 512 == 0 && !getenv("SANIC_GEMM_NO_PRE");
+    int64_t hi_off = 0, lo_off = 0, rs_off = 0;
+    Code kp;
+    kp.indent = 1;
+    if (pre) {
+        hi_off = scratch;
+        scratch += ((M * K * 2 + 255) / 256) * 256;
+        lo_off = scratch;
+        scratch += ((M * K * 2 + 255) / 256) * 256;
+        rs_off = scratch;
+        scratch += ((M * std::max(SR, 1) * 4 + 255) / 256) * 256;
+        kp.line("const int t = threadIdx.x, lane = t & 63, wv = t >> 6;");
+        kp.line("const idx_t mp = (idx_t)blockIdx.x * 4 + wv;");
+        kp.line("unsigned short* ahi = (unsigned short*)((char*)a.scratch + " + std::to_string(hi_off) + ");");
+        kp.line("unsigned short* alo = (unsigned short*)((char*)a.scratch + " + std::to_string(lo_off) + ");");
+        for (int i = 0; i < SR; i++) kp.line("float rp" + std::to_string(i) + " = 0.0f;");
+        for (int64_t i = 0; i < K / 512; i++) {
+            const std::string is = std::to_string(i);
+            const std::string k0 = "(" + std::to_string(i * 512) + " + lane * 8)";
+            kp.line("{");
+            kp.indent++;
+            R.memo.emplace_back();
+            std::vector<std::vector<std::string>> vals(P.rows.size());
+            for (size_t li = 0; li < P.rows.size(); li++) {
+                std::vector<int> rb, rd;
+                bool rok = true, rc = true;
+                std::string rr;
+                Code l1, d1;
+                l1.indent = d1.indent = kp.indent;
+                vals[li] = render_weight_run(d, st.leaf[P.rows[li]], crow[li], {M, K}, l1, d1, "mp", k0, "_p" + std::to_string(li) + "_" + is, rb, rd, rok, rc, rr, false);
+                for (size_t b = 0; b < rb.size(); b++)
+                    kp.line("const " + std::string(ctype_of(rd[b])) + "* __restrict__ wb" + std::to_string(b) + "_p" + std::to_string(li) + "_" + is + " = " + R.param(rb[b]) + ";");
+                kp.s << l1.str() << d1.str();
+            }
+            std::vector<std::string> av(8);
+            for (int j = 0; j < 8; j++) {
+                auto item = [&](int it) -> std::string {
+                    for (size_t li = 0; li < P.rows.size(); li++)
+                        if (P.rows[li] == it) return vals[li][j];
+                    return "0.0f";
+                };
+                av[j] = expr_rest(R, kp, c.into[P.cslots[0]], P.w, item);
+                for (int sidx = 0; sidx < SR; sidx++)
+                    kp.line("rp" + std::to_string(sidx) + " += " + expr_rest(R, kp, c.into[P.rslots[sidx]], -1, item) + ";");
+            }
+            R.memo.pop_back();
+            kp.line("unsigned h_[4], l_[4];");
+            for (int q = 0; q < 4; q++)
+                kp.line("split_bf16(" + av[2 * q] + ", " + av[2 * q + 1] + ", h_[" + std::to_string(q) + "], l_[" + std::to_string(q) + "]);");
+            kp.line("*(sanic_u32x4*)(ahi + mp * " + std::to_string(K) + " + " + k0 + ") = (sanic_u32x4){h_[0], h_[1], h_[2], h_[3]};");
+            kp.line("*(sanic_u32x4*)(alo + mp * " + std::to_string(K) + " + " + k0 + ") = (sanic_u32x4){l_[0], l_[1], l_[2], l_[3]};");
+            kp.indent--;
+            kp.line("}");
+        }
+        for (int i = 0; i < SR; i++) {
+            std::string r = "rp" + std::to_string(i);
+            kp.line("for (int off = 32; off > 0; off >>= 1) " + r + " += __shfl_xor(" + r + ", off, 64);");
+            kp.line("if (lane == 0) ((float*)((char*)a.scratch + " + std::to_string(rs_off) + "))[mp * " + std::to_string(SR) + " + " + std::to_string(i) + "] = " + r + ";");
+        }
+    }
+
     Code k;
     k.indent = 1;
     k.line("__shared__ unsigned short a_lds[2][" + std::to_string(BM * AS) + "];");
@@ -276,7 +340,15 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     auto emit_loads = [&](Code& c2, const std::string& kt0, const std::string& sfx) {
         // A runs
         c2.line("const idx_t mm" + sfx + " = m0 + tid / " + std::to_string(TPR) + ";");
-        for (int r = 0; r < RUNS_A; r++) {
+        for (int r = 0; r < RUNS_A && pre; r++) {
+            std::string k0 = "(" + kt0 + " + (tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8) + ")";
+            const std::string rs = std::to_string(r);
+            c2.line("const sanic_u32x4 pah" + rs + sfx + " = *(const sanic_u32x4*)((const unsigned short*)((const char*)a.scratch + " + std::to_string(hi_off) + ") + mm" + sfx +
+                    " * " + std::to_string(K) + " + " + k0 + ");");
+            c2.line("const sanic_u32x4 pal" + rs + sfx + " = *(const sanic_u32x4*)((const unsigned short*)((const char*)a.scratch + " + std::to_string(lo_off) + ") + mm" + sfx +
+                    " * " + std::to_string(K) + " + " + k0 + ");");
+        }
+        for (int r = 0; r < RUNS_A && !pre; r++) {
             std::string k0 = "(" + kt0 + " + (tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8) + ")";
             for (size_t li = 0; li < P.rows.size(); li++) {
                 std::vector<int> rb, rd;
@@ -340,7 +412,13 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         c2.line("{");
         c2.indent++;
         c2.line("const int ar = tid / " + std::to_string(TPR) + ";");
-        for (int r = 0; r < RUNS_A; r++) {
+        for (int r = 0; r < RUNS_A && pre; r++) {
+            const std::string rs = std::to_string(r);
+            const std::string aoff = "ar * " + std::to_string(AS) + " + (tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8);
+            c2.line("*(sanic_u32x4*)(&a_lds[" + buf + "][" + aoff + "]) = pah" + rs + sfx + ";");
+            c2.line("*(sanic_u32x4*)(&a_lo[" + buf + "][" + aoff + "]) = pal" + rs + sfx + ";");
+        }
+        for (int r = 0; r < RUNS_A && !pre; r++) {
             std::string rs = std::to_string(r);
             // rest of the contraction slot (A) and the row slots, per element
             std::string pk[4];
@@ -462,7 +540,12 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     k.indent--;
     k.line("}");
     // row slots: sum the TPR partial rows, publish per row
-    if (SR) {
+    if (SR && pre) {
+        k.line("for (int i = tid; i < " + std::to_string(BM * SR) + "; i += 256) rs_lds[i] = ((const float*)((const char*)a.scratch + " + std::to_string(rs_off) +
+               "))[m0 * " + std::to_string(SR) + " + i];");
+        k.line("__syncthreads();");
+    }
+    if (SR && !pre) {
         for (int i = 0; i < SR; i++) {
             std::string r = "racc" + std::to_string(i);
             for (int off = 1; off < TPR; off <<= 1) k.line(r + " += __shfl_xor(" + r + ", " + std::to_string(off) + ", 64);");
@@ -517,11 +600,17 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
            "  const unsigned h = pk_bf16(x, y);\n"
            "  hi = h;\n"
            "  lo = pk_bf16(x - __uint_as_float(h << 16), y - __uint_as_float(h & 0xFFFF0000u));\n}\n";
-    src << R.args_struct({});
+    src << R.args_struct(pre ? std::vector<std::string>{"float* __restrict__ scratch"} : std::vector<std::string>{});
+    if (pre) src << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "_pre(Args a) {\n" << R.entry() << kp.str() << "}\n";
     src << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
-    out.kernel_kind = "skeleton:gemm[" + std::to_string(BM) + "x" + std::to_string(BN) + (splitA ? ",a2" : "") + (splitB ? ",b2" : "") + (bkn ? ",kn" : "") + "]";
+    out.kernel_kind = "skeleton:gemm[" + std::to_string(BM) + "x" + std::to_string(BN) + (splitA ? ",a2" : "") + (splitB ? ",b2" : "") + (bkn ? ",kn" : "") + (pre ? ",pre" : "") + "]";
     out.source = src.str();
-    out.launches.push_back({kname, "", dim3((unsigned)((M / BM) * (N / BN))), dim3(256), 0, R.arg_list()});
+    std::vector<Arg> args = R.arg_list();
+    if (pre) {
+        args.push_back({Arg::SCRATCH, 0});
+        out.launches.push_back({kname + "_pre", "", dim3((unsigned)(M / 4)), dim3(256), 0, args});
+    }
+    out.launches.push_back({kname, "", dim3((unsigned)((M / BM) * (N / BN))), dim3(256), 0, args});
     return true;
 }
 

@@ -23,6 +23,7 @@ def _report(exe, got, want):
     (512, 2048, 8192, False),     # same with the reference's [out, in] layout
     (64, 256, 96, True),
     (192, 128, 160, False),
+    (64, 512, 512, True),         # x·g built by the first launch (K % 512 == 0)
 ])
 def test_rmsnorm_gemm(dev, M, K, N, kmajor):
     prog = configs.rmsnorm_projection(M=M, K=K, N=N, kmajor=kmajor)
