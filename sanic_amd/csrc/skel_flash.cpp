@@ -395,14 +395,16 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("const idx_t khi = bhi_a > bhi_b ? bhi_a : bhi_b;");
     k.line("const idx_t wlo = wlo_a < wlo_b ? wlo_a : wlo_b, whi = whi_a > whi_b ? whi_a : whi_b;");
     k.line("const idx_t flo = wlo_a > wlo_b ? wlo_a : wlo_b, fhi = whi_a < whi_b ? whi_a : whi_b;");
-    // Q^T as the B operand: lane = query column l16 (+16·qt), d-slots lq·8 + 0..7 (+32·ds)
-    k.line("bf16x8 qf[2][2];");
+    // Q^T as the B operand (lane = query column l16 (+16·qt), d-slots lq·8 + 0..7 (+32·ds)),
+    // read from LDS each tile rather than held in registers: the block's 128 query rows, 16-byte
+    // chunks XOR-swizzled by row so the 16 rows a lane group reads hit different banks
+    k.line("__shared__ __attribute__((aligned(16))) unsigned short q_lds[128 * 64];");
     k.line("#pragma unroll");
-    k.line("for (int qt = 0; qt < 2; ++qt)");
-    k.line("  #pragma unroll");
-    k.line("  for (int ds = 0; ds < 2; ++ds)");
-    k.line("    qf[qt][ds] = *(const bf16x8*)(" + qp + " + " + std::to_string(P.qacc.addr.c0) + " + " + hterm(qc, qh, qhc) +
-           " + (q0 + qt * 16 + l16) * " + std::to_string(qc[3]) + " + ds * 32 + lq * 8);");
+    k.line("for (int u = 0; u < 4; ++u) {");
+    k.line("  const int ch = tid + u * 256, r = ch >> 3, cc = ch & 7;");
+    k.line("  *(sanic_u32x4*)(&q_lds[r * 64 + ((cc ^ (r & 7)) * 8)]) = *(const sanic_u32x4*)(" + qp + " + " + std::to_string(P.qacc.addr.c0) + " + " +
+           hterm(qc, qh, qhc) + " + (qb * 128 + r) * " + std::to_string(qc[3]) + " + cc * 8);");
+    k.line("}");
     k.line("f32x4 o[4][2];");
     k.line("#pragma unroll");
     k.line("for (int dt = 0; dt < 4; ++dt) { o[dt][0] = (f32x4){0, 0, 0, 0}; o[dt][1] = (f32x4){0, 0, 0, 0}; }");
@@ -474,22 +476,25 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.indent++;
     k.line("const int full = __builtin_amdgcn_readfirstlane((int)(t0 >= flo && t0 + 64 <= fhi));");  // every row sees all
     // S^T tiles: kt (16 keys) × qt (16 queries), contraction over d in 2 steps of 32
+    // scores one query tile at a time (the second tile's accumulators reuse the first's
+    // registers once its softmax is done; the K fragments are re-read from LDS)
     k.line("f32x4 s[4][2];");
-    k.line("#pragma unroll");
-    k.line("for (int kt = 0; kt < 4; ++kt) {");
-    k.line("  s[kt][0] = (f32x4){0, 0, 0, 0}; s[kt][1] = (f32x4){0, 0, 0, 0};");
-    k.line("  #pragma unroll");
-    k.line("  for (int ds = 0; ds < 2; ++ds) {");
-    k.line("    const bf16x8 ka = *(const bf16x8*)(&k_lds[buf][(kt * 16 + l16) * " + std::to_string(KS) + " + ds * 32 + lq * 8]);");
-    k.line("    s[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[0][ds], s[kt][0], 0, 0, 0);");
-    k.line("    s[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[1][ds], s[kt][1], 0, 0, 0);");
-    k.line("  }");
-    k.line("}");
     // online softmax per query column (lane-local; the max reduces across the 4 lane groups)
     k.line("sanic_u32x4 pw[2][2];");
     k.line("#pragma unroll");
     k.line("for (int qt = 0; qt < 2; ++qt) {");
     k.indent++;
+    k.line("#pragma unroll");
+    k.line("for (int kt = 0; kt < 4; ++kt) {");
+    k.line("  s[kt][qt] = (f32x4){0, 0, 0, 0};");
+    k.line("  #pragma unroll");
+    k.line("  for (int ds = 0; ds < 2; ++ds) {");
+    k.line("    const bf16x8 ka = *(const bf16x8*)(&k_lds[buf][(kt * 16 + l16) * " + std::to_string(KS) + " + ds * 32 + lq * 8]);");
+    k.line("    const int qr = wv * 32 + qt * 16 + l16;");
+    k.line("    const bf16x8 qv = *(const bf16x8*)(&q_lds[qr * 64 + (((ds * 4 + lq) ^ (qr & 7)) * 8)]);");
+    k.line("    s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qv, s[kt][qt], 0, 0, 0);");
+    k.line("  }");
+    k.line("}");
     k.line("const int qi = (int)(q0 + qt * 16 + l16);");
     k.line("const int kb = (int)t0 + lq * 4;");
     k.line("float sv[16];");
@@ -631,8 +636,11 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.indent--;
     k.line("}");
 
-    // two waves per SIMD: at most 256 VGPRs, so MFMA of one wave overlaps the softmax of the other
-    src << "extern \"C\" __global__ void __launch_bounds__(256, 2) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
+    // three waves per SIMD: the softmax of one wave overlaps the MFMAs of the others (the
+    // register cap costs a few spilled values outside the inner loop)
+    int occ = 3;
+    if (const char* e = getenv("SANIC_FLASH_OCC")) occ = std::max(1, std::min(4, atoi(e)));
+    src << "extern \"C\" __global__ void __launch_bounds__(256, " << occ << ") " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     out.kernel_kind = "skeleton:flash_prefill[rep " + std::to_string(P.rep) + "]";
     out.source = src.str();
     out.launches.push_back({kname, "", dim3((unsigned)(NH * NQB)), dim3(256), 0, R.arg_list()});
