@@ -83,6 +83,29 @@ def dominant_kernel_roofline(dev, shape, weights, reps=40, copies=8):
             "us_per_launch": secs * 1e6}
 
 
+def cpu_baseline(shape, seconds_budget=20.0):
+    """The oracle's fused f64 decode step (oracle_llama_step) on this host at position 2048."""
+    import ctypes
+    import numpy as np
+    import oracle
+    from tests.llama_ref import OracleModel, synth_weights
+    threads = oracle.threads()
+    w = synth_weights(shape, seed=99)
+    om = OracleModel(shape, w)
+    n, t0 = 0, time.perf_counter()
+    tok = 1
+    while True:
+        tok, _ = om.step(tok, PROMPT + n)
+        n += 1
+        el = time.perf_counter() - t0
+        if el > seconds_budget / 4 or n >= 8:
+            break
+    return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} decode steps of the full model at positions {PROMPT}..{PROMPT + n - 1} "
+                      f"(f64 fused loops over bf16 weights, {threads} threads, "
+                      f"{os.uname().nodename})"}
+
+
 # ── secondary configurations (BASELINE.json configs B, C, D): one dominant kernel each ──
 
 CONFIGS = {
