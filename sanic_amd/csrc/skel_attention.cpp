@@ -325,9 +325,9 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const int64_t NG = NH / REP;
     const int NS = (int)P.scalar_slots.size(), NV = (int)P.vec_slots.size();
     const int PSZ = 1 + NS + NV * (int)E;         // floats per (chunk, head) partial
-    // stream positions per workgroup: 64 (many small workgroups, short phases), doubled until
-    // one group's partials fit the merging workgroup's LDS
-    int CH = 64;
+    // stream positions per workgroup: 128 (measured best at ~2k positions against 64 and 256),
+    // doubled until one group's partials fit the merging workgroup's LDS
+    int CH = 128;
     while (CH < 1024 && ((T + CH - 1) / CH) * REP * PSZ * 4 > 40 * 1024) CH *= 2;
     if (const char* e = getenv("SANIC_ATTN_CH")) CH = std::max(64, std::min(1024, atoi(e) / 64 * 64));
     const int64_t NCH = (T + CH - 1) / CH;
@@ -341,10 +341,10 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     Renderer R(d);
     Code k;
     k.indent = 1;
-    k.line("__shared__ float q_lds[" + std::to_string(REP * HD) + "];");
+    k.line("__shared__ __attribute__((aligned(16))) float q_lds[" + std::to_string(REP * HD) + "];");
     if (wk) k.line("__shared__ float knew_lds[" + std::to_string(HD) + "];");
     if (wvv) k.line("__shared__ float vnew_lds[" + std::to_string(E) + "];");
-    k.line("__shared__ float p_lds[" + std::to_string(REP) + "][" + std::to_string(CH) + "];");
+    k.line("__shared__ __attribute__((aligned(16))) float p_lds[" + std::to_string(REP) + "][" + std::to_string(CH) + "];");
     k.line("__shared__ float stat_lds[" + std::to_string(REP) + "][2];");
     k.line("__shared__ float o_lds[4][" + std::to_string(REP) + "][" + std::to_string(E) + "];");
     k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
@@ -490,10 +490,14 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("  for (int j = 0; j < 8; ++j) kf[j] = knew_lds[d0 + j];");
         k.line("}");
     }
+    // q as 16-byte LDS reads (d0 is a multiple of 8)
     k.line("#pragma unroll");
-    k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r)");
-    k.line("  #pragma unroll");
-    k.line("  for (int j = 0; j < 8; ++j) dot[r] = fmaf(q_lds[r * " + std::to_string(HD) + " + d0 + j], kf[j], dot[r]);");
+    k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) {");
+    k.line("  const sanic_f32x4 qa = *(const sanic_f32x4*)(&q_lds[r * " + std::to_string(HD) + " + d0]);");
+    k.line("  const sanic_f32x4 qb = *(const sanic_f32x4*)(&q_lds[r * " + std::to_string(HD) + " + d0 + 4]);");
+    k.line("  dot[r] = fmaf(qa.x, kf[0], fmaf(qa.y, kf[1], fmaf(qa.z, kf[2], fmaf(qa.w, kf[3], dot[r]))));");
+    k.line("  dot[r] = fmaf(qb.x, kf[4], fmaf(qb.y, kf[5], fmaf(qb.z, kf[6], fmaf(qb.w, kf[7], dot[r]))));");
+    k.line("}");
     k.indent--;
     k.line("}");
     k.line("#pragma unroll");
@@ -559,12 +563,21 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     if (vfast) {
         k.line("if (t0 + tbase + 16 <= t1) {");
         k.line("  const unsigned vw[8] = {vq[sb][0].x, vq[sb][0].y, vq[sb][0].z, vq[sb][0].w, vq[sb][1].x, vq[sb][1].y, vq[sb][1].z, vq[sb][1].w};");
+        // this run's probabilities as 16-byte LDS reads (tbase is a multiple of 16)
+        k.line("  float pr[" + std::to_string(REP) + "][16];");
+        k.line("  #pragma unroll");
+        k.line("  for (int r = 0; r < " + std::to_string(REP) + "; ++r)");
+        k.line("    #pragma unroll");
+        k.line("    for (int q4 = 0; q4 < 4; ++q4) {");
+        k.line("      const sanic_f32x4 pv4 = *(const sanic_f32x4*)(&p_lds[r][tbase + q4 * 4]);");
+        k.line("      pr[r][q4 * 4] = pv4.x; pr[r][q4 * 4 + 1] = pv4.y; pr[r][q4 * 4 + 2] = pv4.z; pr[r][q4 * 4 + 3] = pv4.w;");
+        k.line("    }");
         k.line("  #pragma unroll");
         k.line("  for (int j = 0; j < 16; ++j) {");
         k.line(std::string("    ") + (wvv ? "" : "const ") + "float vf = __uint_as_float((j & 1) ? (vw[j >> 1] & 0xFFFF0000u) : (vw[j >> 1] << 16));");
         if (wvv) k.line("    if (vwriter && t0 + tbase + j == vrow) vf = vnew_lds[e];");
         k.line("    #pragma unroll");
-        k.line("    for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = fmaf(p_lds[r][tbase + j], vf, o[r]);");
+        k.line("    for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = fmaf(pr[r][j], vf, o[r]);");
         k.line("  }");
         k.line("} else {");
         k.line("  for (int j = 0; j < 16; ++j) {");
