@@ -39,6 +39,13 @@ class LlamaMachine:
         self.logits = self.replay.buffer("logits")
         self.token = self.replay.buffer("token")
 
+    @classmethod
+    def from_checkpoint(cls, dev: HipDevice, path: str, shape: configs.LlamaShape = configs.LLAMA_1B, **kw):
+        """A machine over a safetensors checkpoint (HF names; tied embeddings, as
+        llama3_2.rs:88-110 reads them): the weights bind as slices of one device arena."""
+        from . import checkpoint
+        return cls(dev, checkpoint.load_weights(dev, path, shape.weight_shapes()), shape, **kw)
+
     def set_position(self, pos: int):
         self.bind["position"].upload(struct.pack("<f", float(pos)))
 

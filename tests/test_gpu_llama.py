@@ -60,3 +60,26 @@ def test_llama_1b_short_prompt_greedy_ids(full_model):
     # logits are f32 but sit downstream of the bf16 K/V cache: an f32-vs-f64 difference can flip
     # one bf16 rounding of a cache entry (2^-8 relative), so the bf16 bound applies here
     assert worst < 2e-2
+
+
+def test_tiny_llama_from_safetensors_matches_direct_upload(dev, tmp_path):
+    """Weights from a safetensors file (arena slices, one tensor at an unaligned offset and one
+    stored f32, both converted) give the same logits bit for bit as uploading the arrays."""
+    from sanic_amd import checkpoint
+    from sanic_amd.backend import from_bf16_bits
+    w = synth_weights(TINY, seed=5)
+    tensors = {}
+    for i, (name, shp) in enumerate(TINY.weight_shapes()):
+        if i == 1:       # the final norm gain stored f32 (exact in bf16)
+            tensors[name] = ("F32", shp, from_bf16_bits(w[name]).astype(np.float32).tobytes())
+        else:
+            tensors[name] = ("BF16", shp, w[name].tobytes())
+    path = str(tmp_path / "tiny.safetensors")
+    checkpoint.write(path, tensors, align=2)     # leaves some offsets off 16-byte alignment
+    a = LlamaMachine.from_checkpoint(dev, path, TINY)
+    b = _machine(dev, TINY, w)
+    for t in [3, 17, 250, 9, 44]:
+        a.step(t)
+        b.step(t)
+        assert np.array_equal(a.last_logits(), b.last_logits())
+        assert a.last_token() == b.last_token()
