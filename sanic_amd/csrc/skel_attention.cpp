@@ -331,13 +331,30 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     while (CH < 1024 && ((T + CH - 1) / CH) * REP * PSZ * 4 > 40 * 1024) CH *= 2;
     if (const char* e = getenv("SANIC_ATTN_CH")) CH = std::max(64, std::min(1024, atoi(e) / 64 * 64));
     const int64_t NCH = (T + CH - 1) / CH;
-    int64_t part_off = scratch;
-    scratch += ((NCH * NH * PSZ * 4 + 255) / 256) * 256;
-
     const std::vector<RowWrite> writes = absorbed_writes(d, si, P);
     bool wk = false, wvv = false;
     for (auto& w : writes) (w.is_k ? wk : wvv) = true;
     if (wvv && !(P.vacc.dtype == SANIC_BF16)) return false;
+    // Separate row writer: when this step's K row and V column are absorbed at the same
+    // position, one extra workgroup per KV group (chunk index NCH) computes and stores them and
+    // contributes that single position as its own partial carrier (m = its score, ℓ = 1, o = its
+    // value row); the regular chunks leave the position out. No regular chunk then waits on the
+    // row's loads and RoPE arithmetic, which otherwise put the chunk holding the row last.
+    bool sep = wk && wvv && !getenv("SANIC_ATTN_INCHUNK_WRITE");
+    if (sep) {
+        std::string rp[2];
+        for (int i = 0; i < 2; i++) {
+            Renderer R2(d);
+            Code c2;
+            const sanic_node& pn = d->nodes[writes[i].pos];
+            rp[i] = R2.value(c2, writes[i].pos, std::vector<std::string>(pn.rank, "0"));
+            rp[i] = c2.str() + "|" + rp[i];
+        }
+        sep = rp[0] == rp[1];
+    }
+    const int64_t NPART = NCH + (sep ? 1 : 0);   // partial carriers per KV group
+    int64_t part_off = scratch;
+    scratch += ((NPART * NH * PSZ * 4 + 255) / 256) * 256;
     Renderer R(d);
     Code k;
     k.indent = 1;
@@ -368,15 +385,13 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     }
     k.line("const idx_t t0 = lo0 + chunk * " + std::to_string(CH) + ";");
     k.line("float* part = a.scratch + " + std::to_string(part_off / 4) + " + (chunk * " + std::to_string(NH) + " + grp * " + std::to_string(REP) + ") * " + std::to_string(PSZ) + ";");
-    // identity partial for chunks past the visible window
-    k.line("if (t0 >= hi0) {");
-    k.line("  for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += 256) {");
-    k.line("    const int r = i / " + std::to_string(PSZ) + ", f = i % " + std::to_string(PSZ) + ";");
-    k.line("    sanic_st(part + r * " + std::to_string(PSZ) + " + f, f == 0 ? " + flit(c.identity[P.max_slot]) + " : 0.0f);");
-    k.line("  }");
-    k.line("} else {");
-    k.line("const idx_t t1 = t0 + " + std::to_string(CH) + " < hi0 ? t0 + " + std::to_string(CH) + " : hi0;");
-    // ── prefetch: every K row and V run of this chunk is requested before any compute ──
+    // ── prefetch: every K row and V run of this chunk is requested before any compute. When the
+    // window has no lower edge (causal / decode prefix) the chunk's rows do not depend on the
+    // position, so the requests go out before the position load returns; addresses are clamped
+    // to the cache capacity and every use below still tests the window.
+    bool lo_static = true;
+    for (auto& b : win) lo_static &= b.kind != WindowBound::LO_CEIL;
+    const std::string tpre = lo_static ? "((idx_t)chunk * " + std::to_string(CH) + ")" : "t0";
     const int LPT = 4;                                   // lanes per key position
     const int64_t DPL = HD / LPT;                        // contiguous d per lane (multiple of 8)
     const int NP = CH / 64;                              // score passes (64 positions each)
@@ -391,26 +406,29 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
            " + grp * " + std::to_string(vh) + ";");
     k.line("const int sub = tid % " + std::to_string(LPT) + ";");
     k.line("sanic_u32x4 kq[" + std::to_string(NP) + "][" + std::to_string(DPL / 8) + "];");
+    if (vfast) k.line("sanic_u32x4 vq[" + std::to_string(NP) + "][2];");
+    k.line("const int e_ = tid % 64, tg = tid / 64;");   // value phase: lane = value dim, 4 groups of CH/4 positions
+    if (sep) k.line("if (chunk < " + std::to_string(NCH) + ") {   // the row writer streams nothing");
     k.line("#pragma unroll");
     k.line("for (int ps = 0; ps < " + std::to_string(NP) + "; ++ps) {");
-    k.line("  const idx_t t = t0 + ps * 64 + tid / " + std::to_string(LPT) + ";");
-    k.line("  const idx_t tt = t < t1 ? t : t0;");
+    k.line("  const idx_t t = " + tpre + " + ps * 64 + tid / " + std::to_string(LPT) + ";");
+    k.line("  const idx_t tt = t < " + std::to_string(T) + " ? t : 0;");
     k.line("  #pragma unroll");
     k.line("  for (int v8 = 0; v8 < " + std::to_string(DPL / 8) + "; ++v8)");
     k.line("    kq[ps][v8] = *(const sanic_u32x4*)(kp + tt * " + std::to_string(kt) + " + sub * " + std::to_string(DPL) + " + v8 * 8);");
     k.line("}");
-    k.line("const int e_ = tid % 64, tg = tid / 64;");   // value phase: lane = value dim, 4 groups of CH/4 positions
     if (vfast) {
-        k.line("sanic_u32x4 vq[" + std::to_string(NP) + "][2];");
         k.line("#pragma unroll");
         k.line("for (int sb = 0; sb < " + std::to_string(NP) + "; ++sb) {");
-        k.line("  const idx_t tb = t0 + tg * " + std::to_string(CH / 4) + " + sb * 16;");
-        k.line("  const bool full = tb + 16 <= t1 && e_ < " + std::to_string(E) + ";");
+        k.line("  const idx_t tb = " + tpre + " + tg * " + std::to_string(CH / 4) + " + sb * 16;");
+        k.line("  const bool full = tb + 16 <= " + std::to_string(T) + " && e_ < " + std::to_string(E) + ";");
         k.line("  const unsigned short* src = vp + (full ? (idx_t)e_ * " + std::to_string(ve) + " + tb : 0);");
         k.line("  vq[sb][0] = *(const sanic_u32x4*)(src);");
         k.line("  vq[sb][1] = *(const sanic_u32x4*)(src + 8);");
         k.line("}");
     }
+    if (sep) k.line("}");
+    auto emit_writes = [&](bool force) {
     // absorbed row writes: the workgroup whose chunk holds the row (chunk 0 when the row is
     // outside the window) computes and stores this group's row elements
     for (auto& w : writes) {
@@ -424,7 +442,8 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         R.memo.pop_back();
         k.line("const float " + nm + "pf = roundf(" + pv + ");");
         k.line("const idx_t " + nm + "row = (" + nm + "pf >= 0.0f && " + nm + "pf < " + std::to_string(T) + ".0f) ? (idx_t)" + nm + "pf : -1;");
-        k.line("const bool " + nm + "writer = " + nm + "row >= 0 && chunk == ((" + nm + "row >= lo0 && " + nm + "row < hi0) ? (" + nm + "row - lo0) / " +
+        if (force) k.line("const bool " + nm + "writer = " + nm + "row >= 0;");
+        else k.line("const bool " + nm + "writer = " + nm + "row >= 0 && chunk == ((" + nm + "row >= lo0 && " + nm + "row < hi0) ? (" + nm + "row - lo0) / " +
                std::to_string(CH) + " : 0);");
         k.line("if (" + nm + "writer) {");
         k.indent++;
@@ -454,6 +473,8 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.indent--;
         k.line("}");
     }
+    };
+    auto emit_q = [&]() {
     // query vectors (the A side, rendered) into LDS, after the K/V prefetch is issued: its latency hides behind the q-side arithmetic
     if (REP * HD == 256) k.line("{ const int i = tid;");
     else k.line("for (int i = tid; i < " + std::to_string(REP * HD) + "; i += 256) {");
@@ -468,6 +489,80 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     }
     k.indent--;
     k.line("}");
+    };
+    if (sep) {
+        k.line("if (chunk == " + std::to_string(NCH) + ") {");
+        k.indent++;
+        emit_q();
+        emit_writes(true);
+        k.line("__syncthreads();");
+        k.line("const bool nvis = krow >= 0 && krow >= lo0 && krow < hi0;");
+        for (int r = 0; r < REP; r++) {
+            // score of head grp·REP + r at the new row (wave r % 4), the leaf with its contraction substituted
+            k.line("if (wv == " + std::to_string(r % 4) + ") {");
+            k.indent++;
+            k.line("float dv = 0.0f;");
+            k.line("for (int dd = lane; dd < " + std::to_string(HD) + "; dd += 64) dv = fmaf(q_lds[" + std::to_string(r * HD) + " + dd], knew_lds[dd], dv);");
+            k.line("for (int off = 32; off > 0; off >>= 1) dv += __shfl_xor(dv, off, 64);");
+            k.line("if (lane == 0) {");
+            k.indent++;
+            k.line("const float dotv = dv;");
+            k.line("const idx_t s = krow < 0 ? 0 : krow;");
+            R.memo.emplace_back();
+            R.subst[P.dot.reduce] = "dotv";
+            const sanic_node& sl = d->nodes[st.leaf[P.sleaf]];
+            std::vector<std::string> lc(sl.rank);
+            for (int j = 0; j < sl.rank; j++) {
+                int bd = st.bind[P.sleaf][j];
+                lc[j] = bd == SANIC_BIND_STREAM ? "s" : bd == P.hdim ? "(grp * " + std::to_string(REP) + " + " + std::to_string(r) + ")" : "0";
+            }
+            std::string v = R.value(k, st.leaf[P.sleaf], lc);
+            R.subst.clear();
+            R.memo.pop_back();
+            k.line("stat_lds[" + std::to_string(r) + "][0] = nvis ? " + v + " : (-__builtin_huge_valf());");
+            k.indent--;
+            k.line("}");
+            k.indent--;
+            k.line("}");
+        }
+        k.line("__syncthreads();");
+        // the one-position partial: m = score, scalar slots into·1, vector slots the value row
+        k.line("for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += 256) {");
+        k.indent++;
+        k.line("const int r = i / " + std::to_string(PSZ) + ", f = i % " + std::to_string(PSZ) + ";");
+        k.line("const float m = stat_lds[r][0];");
+        k.line("const bool live = (-__builtin_huge_valf()) < m;");
+        k.line("float v;");
+        k.line("if (f == 0) v = m;");
+        for (int sidx = 0; sidx < NS; sidx++)
+            k.line("else if (f == " + std::to_string(1 + sidx) + ") v = live ? " + flit(P.scalar_into[sidx]) + " : 0.0f;");
+        k.line("else v = live ? vnew_lds[(f - " + std::to_string(1 + NS) + ") % " + std::to_string(E) + "] : 0.0f;");
+        k.line("sanic_st(part + r * " + std::to_string(PSZ) + " + f, v);");
+        k.indent--;
+        k.line("}");
+        k.indent--;
+        k.line("} else");
+    }
+    // identity partial for chunks past the visible window
+    k.line("if (t0 >= hi0) {");
+    k.line("  for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += 256) {");
+    k.line("    const int r = i / " + std::to_string(PSZ) + ", f = i % " + std::to_string(PSZ) + ";");
+    k.line("    sanic_st(part + r * " + std::to_string(PSZ) + " + f, f == 0 ? " + flit(c.identity[P.max_slot]) + " : 0.0f);");
+    k.line("  }");
+    k.line("} else {");
+    k.line("const idx_t t1 = t0 + " + std::to_string(CH) + " < hi0 ? t0 + " + std::to_string(CH) + " : hi0;");
+    if (sep) {
+        // the new row's position: excluded here, folded by the writer workgroup
+        R.memo.emplace_back();
+        const sanic_node& pn = d->nodes[writes[0].pos];
+        std::string pv = R.value(k, writes[0].pos, std::vector<std::string>(pn.rank, "0"));
+        R.memo.pop_back();
+        k.line("const float npf = roundf(" + pv + ");");
+        k.line("const idx_t nrow = (npf >= 0.0f && npf < " + std::to_string(T) + ".0f) ? (idx_t)npf : -1;");
+    } else {
+        emit_writes(false);
+    }
+    emit_q();
     k.line("__syncthreads();");
     // scores
     k.line("#pragma unroll");
@@ -484,7 +579,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("const int d0 = sub * " + std::to_string(DPL) + " + v8 * 8;");
     k.line("const sanic_u32x4 kv = kq[ps][v8];");
     k.line(std::string(wk ? "" : "const ") + "float kf[8] = {__uint_as_float(kv.x << 16), __uint_as_float(kv.x & 0xFFFF0000u), __uint_as_float(kv.y << 16), __uint_as_float(kv.y & 0xFFFF0000u), __uint_as_float(kv.z << 16), __uint_as_float(kv.z & 0xFFFF0000u), __uint_as_float(kv.w << 16), __uint_as_float(kv.w & 0xFFFF0000u)};");
-    if (wk) {
+    if (wk && !sep) {
         k.line("if (kwriter && t == krow) {");
         k.line("  #pragma unroll");
         k.line("  for (int j = 0; j < 8; ++j) kf[j] = knew_lds[d0 + j];");
@@ -524,7 +619,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         std::string v = R.value(k, st.leaf[P.sleaf], lc);
         R.subst.clear();
         R.memo.pop_back();
-        k.line("p_lds[" + std::to_string(r) + "][tl] = t < t1 ? " + v + " : (-__builtin_huge_valf());");
+        k.line("p_lds[" + std::to_string(r) + "][tl] = " + std::string(sep ? "t < t1 && t != nrow" : "t < t1") + " ? " + v + " : (-__builtin_huge_valf());");
         k.indent--;
         k.line("}");
     }
@@ -561,7 +656,11 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.indent++;
     k.line("const int tbase = tg * " + std::to_string(CH / 4) + " + sb * 16;");
     if (vfast) {
-        k.line("if (t0 + tbase + 16 <= t1) {");
+        // the prefetched run covers the block whenever it lies inside the cache; positions past
+        // the window contribute nothing (their value is masked to 0 and their probability is 0)
+        k.line("if (t0 + tbase + 16 <= " + std::to_string(T) + ") {");
+        if (sep) k.line("  const bool partial = t0 + tbase + 16 > t1 || (nrow >= t0 + tbase && nrow < t0 + tbase + 16);");
+        else k.line("  const bool partial = t0 + tbase + 16 > t1;");
         k.line("  const unsigned vw[8] = {vq[sb][0].x, vq[sb][0].y, vq[sb][0].z, vq[sb][0].w, vq[sb][1].x, vq[sb][1].y, vq[sb][1].z, vq[sb][1].w};");
         // this run's probabilities as 16-byte LDS reads (tbase is a multiple of 16)
         k.line("  float pr[" + std::to_string(REP) + "][16];");
@@ -574,17 +673,19 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("    }");
         k.line("  #pragma unroll");
         k.line("  for (int j = 0; j < 16; ++j) {");
-        k.line(std::string("    ") + (wvv ? "" : "const ") + "float vf = __uint_as_float((j & 1) ? (vw[j >> 1] & 0xFFFF0000u) : (vw[j >> 1] << 16));");
-        if (wvv) k.line("    if (vwriter && t0 + tbase + j == vrow) vf = vnew_lds[e];");
+        k.line("    float vf = __uint_as_float((j & 1) ? (vw[j >> 1] & 0xFFFF0000u) : (vw[j >> 1] << 16));");
+        if (wvv && !sep) k.line("    if (vwriter && t0 + tbase + j == vrow) vf = vnew_lds[e];");
+        if (sep) k.line("    if (partial && (t0 + tbase + j >= t1 || t0 + tbase + j == nrow)) vf = 0.0f;");
+        else k.line("    if (partial && t0 + tbase + j >= t1) vf = 0.0f;");
         k.line("    #pragma unroll");
         k.line("    for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = fmaf(pr[r][j], vf, o[r]);");
         k.line("  }");
         k.line("} else {");
         k.line("  for (int j = 0; j < 16; ++j) {");
         k.line("    const idx_t t = t0 + tbase + j;");
-        k.line("    if (t < t1) {");
+        k.line(std::string("    if (t < t1") + (sep ? " && t != nrow" : "") + ") {");
         k.line(std::string("      ") + (wvv ? "" : "const ") + "float vf = sanic_bf16(vp[e * " + std::to_string(ve) + " + t]);");
-        if (wvv) k.line("      if (vwriter && t == vrow) vf = vnew_lds[e];");
+        if (wvv && !sep) k.line("      if (vwriter && t == vrow) vf = vnew_lds[e];");
         k.line("      for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = fmaf(p_lds[r][tbase + j], vf, o[r]);");
         k.line("    }");
         k.line("  }");
@@ -592,9 +693,9 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     } else {
         k.line("for (int j = 0; j < 16; ++j) {");
         k.line("  const idx_t t = t0 + tbase + j;");
-        k.line("  if (t < t1) {");
+        k.line(std::string("  if (t < t1") + (sep ? " && t != nrow" : "") + ") {");
         k.line(std::string("    ") + (wvv ? "" : "const ") + "float vf = sanic_bf16(vp[e * " + std::to_string(ve) + " + t * " + std::to_string(vt) + "]);");
-        if (wvv) k.line("    if (vwriter && t == vrow) vf = vnew_lds[e];");
+        if (wvv && !sep) k.line("    if (vwriter && t == vrow) vf = vnew_lds[e];");
         k.line("    for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = fmaf(p_lds[r][tbase + j], vf, o[r]);");
         k.line("  }");
         k.line("}");
@@ -627,7 +728,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     // (interp.rs:555-643) regrouped — no chain of NCH dependent steps.
     int64_t counter_off = scratch;
     scratch += ((NG * 4 + 255) / 256) * 256;
-    const int64_t GP = NCH * REP * PSZ;       // floats of one group's partials
+    const int64_t GP = NPART * REP * PSZ;       // floats of one group's partials
     if (GP * 4 > 64 * 1024) return false;
     k.line("{");
     k.indent++;
@@ -635,28 +736,28 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("__builtin_amdgcn_s_waitcnt(0);");
     k.line("__syncthreads();");
     k.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(counter_off) + ") + grp;");
-    k.line("if (tid == 0) sanic_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == " + std::to_string(NCH) + "u - 1u;");
+    k.line("if (tid == 0) sanic_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == " + std::to_string(NPART) + "u - 1u;");
     k.line("__syncthreads();");
     k.line("if (!sanic_last) return;");
     k.line("__shared__ __attribute__((aligned(16))) float g_lds[" + std::to_string(GP) + "];");
-    k.line("__shared__ float w_lds[" + std::to_string(REP) + "][" + std::to_string(NCH) + "];");
+    k.line("__shared__ float w_lds[" + std::to_string(REP) + "][" + std::to_string(NPART) + "];");
     k.line("__shared__ float mx_lds[" + std::to_string(REP) + "];");
     // every coherent load is issued before the first is consumed (one round trip, not GP/256):
     // 16-byte loads when a chunk's group partials are 16-byte aligned runs
     if ((REP * PSZ) % 4 == 0 && (NH * PSZ) % 4 == 0 && part_off % 16 == 0) {
         const int64_t Q4 = REP * PSZ / 4;                     // float4 per chunk
-        const int64_t PER = (NCH * Q4 + 255) / 256;
+        const int64_t PER = (NPART * Q4 + 255) / 256;
         k.line("const float* gbase = a.scratch + " + std::to_string(part_off / 4) + " + grp * " + std::to_string(REP * PSZ) + ";");
         k.line("sanic_f32x4 gv[" + std::to_string(PER) + "];");
         k.line("#pragma unroll");
         k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j) {");
         k.line("  const int i = tid + j * 256;");
         k.line("  const int ch = i / " + std::to_string(Q4) + ", w = i % " + std::to_string(Q4) + ";");
-        k.line("  gv[j] = sanic_ld4(gbase, (unsigned)((i < " + std::to_string(NCH * Q4) + " ? ch * " + std::to_string(NH * PSZ) + " + w * 4 : 0) * 4));");
+        k.line("  gv[j] = sanic_ld4(gbase, (unsigned)((i < " + std::to_string(NPART * Q4) + " ? ch * " + std::to_string(NH * PSZ) + " + w * 4 : 0) * 4));");
         k.line("}");
         k.line("#pragma unroll");
         k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j)");
-        k.line("  if (tid + j * 256 < " + std::to_string(NCH * Q4) + ") *(sanic_f32x4*)(g_lds + (tid + j * 256) * 4) = gv[j];");
+        k.line("  if (tid + j * 256 < " + std::to_string(NPART * Q4) + ") *(sanic_f32x4*)(g_lds + (tid + j * 256) * 4) = gv[j];");
     } else {
         const int64_t PER = (GP + 255) / 256;
         k.line("float gv[" + std::to_string(PER) + "];");
@@ -677,9 +778,9 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("for (int r = wv; r < " + std::to_string(REP) + "; r += 4) {");
     k.indent++;
     k.line("float m = (-__builtin_huge_valf());");
-    k.line("for (int ch = lane; ch < " + std::to_string(NCH) + "; ch += 64) m = fmaxf(m, g_lds[(ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + "]);");
+    k.line("for (int ch = lane; ch < " + std::to_string(NPART) + "; ch += 64) m = fmaxf(m, g_lds[(ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + "]);");
     k.line("for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));");
-    k.line("for (int ch = lane; ch < " + std::to_string(NCH) + "; ch += 64) {");
+    k.line("for (int ch = lane; ch < " + std::to_string(NPART) + "; ch += 64) {");
     k.line("  const float mc = g_lds[(ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + "];");
     k.line("  w_lds[r][ch] = (-__builtin_huge_valf()) < mc ? __builtin_amdgcn_exp2f((mc - m) * 1.44269504088896341f) : 0.0f;");
     k.line("}");
@@ -708,7 +809,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         if (sidx == P.max_slot) { k.line("const float acc" + ss + " = mx_lds[r];"); continue; }
         k.line("float acc" + ss + " = 0.0f;");
     }
-    k.line("for (int ch = 0; ch < " + std::to_string(NCH) + "; ++ch) {");
+    k.line("for (int ch = 0; ch < " + std::to_string(NPART) + "; ++ch) {");
     k.line("  const float wc = w_lds[r][ch];");
     k.line("  const float* pc = g_lds + (ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + ";");
     for (int sidx = 0; sidx < c.slots; sidx++) {
@@ -739,11 +840,11 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     std::ostringstream src;
     src << kPrelude << R.args_struct({"float* __restrict__ scratch"});
     src << "extern \"C\" __global__ void __launch_bounds__(256) " << kpart << "(Args a) {\n" << R.entry() << k.str() << "}\n";
-    out.kernel_kind = "skeleton:attn_decode[rep " + std::to_string(REP) + "]" + (writes.empty() ? "" : "+writes" + std::to_string(writes.size()));
+    out.kernel_kind = "skeleton:attn_decode[rep " + std::to_string(REP) + "]" + (writes.empty() ? "" : "+writes" + std::to_string(writes.size())) + (sep ? "+rowwg" : "");
     out.source = src.str();
     std::vector<Arg> args = R.arg_list();
     args.push_back({Arg::SCRATCH, 0});
-    out.launches.push_back({kpart, "", dim3((unsigned)NG, (unsigned)NCH), dim3(256), 0, args});
+    out.launches.push_back({kpart, "", dim3((unsigned)NG, (unsigned)NPART), dim3(256), 0, args});
     return true;
 }
 
