@@ -15,6 +15,9 @@
 //                partials with the carrier's own rendered combine (−∞ guard included), projects,
 //                runs the epilogue and stores. Oracle: interp.rs:555-643 run_carrier_split.
 #include <algorithm>
+#include <regex>
+#include <set>
+#include <sstream>
 #include <cmath>
 
 #include "emit.h"
@@ -327,9 +330,14 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const int PSZ = 1 + NS + NV * (int)E;         // floats per (chunk, head) partial
     // stream positions per workgroup: 128 (measured best at ~2k positions against 64 and 256),
     // doubled until one group's partials fit the merging workgroup's LDS
-    int CH = 128;
+    // threads per workgroup: 1024 (16 waves, four per SIMD, so the dependent LDS/shuffle phases
+    // of one wave hide behind the others'), over 256-position chunks
+    int NT = 1024;
+    if (const char* e = getenv("SANIC_ATTN_NT")) NT = atoi(e) >= 1024 ? 1024 : atoi(e) >= 512 ? 512 : 256;
+    const int NW = NT / 64;
+    int CH = NT / 4;
     while (CH < 1024 && ((T + CH - 1) / CH) * REP * PSZ * 4 > 40 * 1024) CH *= 2;
-    if (const char* e = getenv("SANIC_ATTN_CH")) CH = std::max(64, std::min(1024, atoi(e) / 64 * 64));
+    if (const char* e = getenv("SANIC_ATTN_CH")) CH = std::max(NT / 4, std::min(1024, atoi(e) / (NT / 4) * (NT / 4)));
     const int64_t NCH = (T + CH - 1) / CH;
     const std::vector<RowWrite> writes = absorbed_writes(d, si, P);
     bool wk = false, wvv = false;
@@ -363,7 +371,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     if (wvv) k.line("__shared__ float vnew_lds[" + std::to_string(E) + "];");
     k.line("__shared__ __attribute__((aligned(16))) float p_lds[" + std::to_string(REP) + "][" + std::to_string(CH) + "];");
     k.line("__shared__ float stat_lds[" + std::to_string(REP) + "][2];");
-    k.line("__shared__ float o_lds[4][" + std::to_string(REP) + "][" + std::to_string(E) + "];");
+    k.line("__shared__ float o_lds[" + std::to_string(NW) + "][" + std::to_string(REP) + "][" + std::to_string(E) + "];");
     k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
     k.line("const idx_t grp = blockIdx.x, chunk = blockIdx.y;");
     // honest window (per first head of the group; bounds not depending on the head)
@@ -394,7 +402,10 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const std::string tpre = lo_static ? "((idx_t)chunk * " + std::to_string(CH) + ")" : "t0";
     const int LPT = 4;                                   // lanes per key position
     const int64_t DPL = HD / LPT;                        // contiguous d per lane (multiple of 8)
-    const int NP = CH / 64;                              // score passes (64 positions each)
+    const int PPP = NT / LPT;                            // key positions per score pass
+    const int NP = CH / PPP;                             // score passes
+    const int PG = CH / NW;                              // value phase: positions per wave group
+    const int NSB = PG / 16;                             // 16-position runs per value group
     int repk; int64_t kt, kd, kh;
     addr_parts(P.dot.kacc.addr, repk, NH, kt, kd, kh);
     int repv; int64_t vt, ve, vh;
@@ -405,29 +416,6 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("const unsigned short* __restrict__ vp = " + R.param(P.vacc.buffer) + " + " + std::to_string(P.vacc.addr.c0) +
            " + grp * " + std::to_string(vh) + ";");
     k.line("const int sub = tid % " + std::to_string(LPT) + ";");
-    k.line("sanic_u32x4 kq[" + std::to_string(NP) + "][" + std::to_string(DPL / 8) + "];");
-    if (vfast) k.line("sanic_u32x4 vq[" + std::to_string(NP) + "][2];");
-    k.line("const int e_ = tid % 64, tg = tid / 64;");   // value phase: lane = value dim, 4 groups of CH/4 positions
-    if (sep) k.line("if (chunk < " + std::to_string(NCH) + ") {   // the row writer streams nothing");
-    k.line("#pragma unroll");
-    k.line("for (int ps = 0; ps < " + std::to_string(NP) + "; ++ps) {");
-    k.line("  const idx_t t = " + tpre + " + ps * 64 + tid / " + std::to_string(LPT) + ";");
-    k.line("  const idx_t tt = t < " + std::to_string(T) + " ? t : 0;");
-    k.line("  #pragma unroll");
-    k.line("  for (int v8 = 0; v8 < " + std::to_string(DPL / 8) + "; ++v8)");
-    k.line("    kq[ps][v8] = *(const sanic_u32x4*)(kp + tt * " + std::to_string(kt) + " + sub * " + std::to_string(DPL) + " + v8 * 8);");
-    k.line("}");
-    if (vfast) {
-        k.line("#pragma unroll");
-        k.line("for (int sb = 0; sb < " + std::to_string(NP) + "; ++sb) {");
-        k.line("  const idx_t tb = " + tpre + " + tg * " + std::to_string(CH / 4) + " + sb * 16;");
-        k.line("  const bool full = tb + 16 <= " + std::to_string(T) + " && e_ < " + std::to_string(E) + ";");
-        k.line("  const unsigned short* src = vp + (full ? (idx_t)e_ * " + std::to_string(ve) + " + tb : 0);");
-        k.line("  vq[sb][0] = *(const sanic_u32x4*)(src);");
-        k.line("  vq[sb][1] = *(const sanic_u32x4*)(src + 8);");
-        k.line("}");
-    }
-    if (sep) k.line("}");
     auto emit_writes = [&](bool force) {
     // absorbed row writes: the workgroup whose chunk holds the row (chunk 0 when the row is
     // outside the window) computes and stores this group's row elements
@@ -447,7 +435,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
                std::to_string(CH) + " : 0);");
         k.line("if (" + nm + "writer) {");
         k.indent++;
-        k.line("for (int xw = tid; xw < " + std::to_string(X) + "; xw += 256) {");
+        k.line("for (int xw = tid; xw < " + std::to_string(X) + "; xw += " + std::to_string(NT) + ") {");
         k.indent++;
         k.line("const idx_t wf = " + addr.render({"(grp * " + std::to_string(REP) + ")", nm + "row", "xw"}) + ";");
         std::vector<std::string> wc;
@@ -474,32 +462,95 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("}");
     }
     };
+    // query vectors (the A side, rendered) into LDS. With one element per thread the rendered
+    // code is split: index arithmetic and plain buffer loads go out ahead of the K/V prefetch
+    // (loads complete in issue order, so a q load issued after the prefetch would wait for all of
+    // it), the arithmetic (RoPE, with its branchy sin/cos) runs after the prefetch is issued.
+    std::string q_post;
     auto emit_q = [&]() {
-    // query vectors (the A side, rendered) into LDS, after the K/V prefetch is issued: its latency hides behind the q-side arithmetic
-    if (REP * HD == 256) k.line("{ const int i = tid;");
-    else k.line("for (int i = tid; i < " + std::to_string(REP * HD) + "; i += 256) {");
-    k.indent++;
-    k.line("const idx_t hq = grp * " + std::to_string(REP) + " + i / " + std::to_string(HD) + ";");
-    k.line("const idx_t dd = i % " + std::to_string(HD) + ";");
-    {
+        if (REP * HD != 256) {
+            k.line("for (int i = tid; i < " + std::to_string(REP * HD) + "; i += " + std::to_string(NT) + ") {");
+            k.indent++;
+            k.line("const idx_t hq = grp * " + std::to_string(REP) + " + i / " + std::to_string(HD) + ";");
+            k.line("const idx_t dd = i % " + std::to_string(HD) + ";");
+            R.memo.emplace_back();
+            std::string v = R.value(k, P.dot.a, P.dot.a_coords);
+            R.memo.pop_back();
+            k.line("q_lds[i] = " + v + ";");
+            k.indent--;
+            k.line("}");
+            return;
+        }
+        k.line("const int qt = tid & 255;");
+        k.line("const idx_t hq = grp * " + std::to_string(REP) + " + qt / " + std::to_string(HD) + ";");
+        k.line("const idx_t dd = qt % " + std::to_string(HD) + ";");
+        Code tmp;
+        tmp.indent = 0;
         R.memo.emplace_back();
-        std::string v = R.value(k, P.dot.a, P.dot.a_coords);
+        std::string v = R.value(tmp, P.dot.a, P.dot.a_coords);
         R.memo.pop_back();
-        k.line("q_lds[i] = " + v + ";");
-    }
-    k.indent--;
-    k.line("}");
+        std::set<std::string> known = {"hq", "dd", "qt", "grp", "tid", "lane", "wv", "chunk"};
+        std::istringstream in(tmp.str());
+        std::string ln, post;
+        static const std::regex decl(R"(^\s*const (idx_t|int|float) (\w+) = (.*);\s*$)");
+        static const std::regex load(R"(^a\.b\d+\[\(idx_t\)\((\w+)\)\]$)");
+        static const std::regex ident(R"([A-Za-z_]\w*)");
+        static const std::regex call(R"([A-Za-z_]\w*\s*\()");
+        while (std::getline(in, ln)) {
+            std::smatch m;
+            bool hoist = false;
+            if (std::regex_match(ln, m, decl)) {
+                const std::string ty = m[1], name = m[2], rhs = m[3];
+                bool ok = ty != "float" || std::regex_match(rhs, load);
+                std::string r2 = std::regex_replace(rhs, std::regex(R"(a\.b\d+)"), " ");
+                ok = ok && !std::regex_search(r2, call);
+                for (auto it = std::sregex_iterator(r2.begin(), r2.end(), ident); ok && it != std::sregex_iterator(); ++it) {
+                    const std::string id = it->str();
+                    if (id == "idx_t" || id == "float" || id == "int") continue;
+                    if (!known.count(id) && !(id.size() > 2 && id[0] == 's' && id[1] == 'c' && isdigit((unsigned char)id[2]))) ok = false;
+                }
+                if (ok) {
+                    hoist = true;
+                    known.insert(name);
+                }
+            }
+            if (hoist) k.line(ln.substr(ln.find_first_not_of(' ')));
+            else post += "  " + ln + "\n";
+        }
+        q_post = post + (NT > 256 ? "  if (tid < 256) q_lds[qt] = " : "  q_lds[qt] = ") + v + ";\n";
     };
+    emit_q();
+    k.line("sanic_u32x4 kq[" + std::to_string(NP) + "][" + std::to_string(DPL / 8) + "];");
+    if (vfast) k.line("sanic_u32x4 vq[" + std::to_string(NSB) + "][2];");
+    k.line("const int e_ = tid % 64, tg = tid / 64;");   // value phase: lane = value dim, 4 groups of CH/4 positions
+    k.line("#pragma unroll");
+    k.line("for (int ps = 0; ps < " + std::to_string(NP) + "; ++ps) {");
+    k.line("  const idx_t t = " + tpre + " + ps * " + std::to_string(PPP) + " + tid / " + std::to_string(LPT) + ";");
+    k.line("  const idx_t tt = t < " + std::to_string(T) + " ? t : 0;");
+    k.line("  #pragma unroll");
+    k.line("  for (int v8 = 0; v8 < " + std::to_string(DPL / 8) + "; ++v8)");
+    k.line("    kq[ps][v8] = *(const sanic_u32x4*)(kp + tt * " + std::to_string(kt) + " + sub * " + std::to_string(DPL) + " + v8 * 8);");
+    k.line("}");
+    if (vfast) {
+        k.line("#pragma unroll");
+        k.line("for (int sb = 0; sb < " + std::to_string(NSB) + "; ++sb) {");
+        k.line("  const idx_t tb = " + tpre + " + tg * " + std::to_string(PG) + " + sb * 16;");
+        k.line("  const bool full = tb + 16 <= " + std::to_string(T) + " && e_ < " + std::to_string(E) + ";");
+        k.line("  const unsigned short* src = vp + (full ? (idx_t)e_ * " + std::to_string(ve) + " + tb : 0);");
+        k.line("  vq[sb][0] = *(const sanic_u32x4*)(src);");
+        k.line("  vq[sb][1] = *(const sanic_u32x4*)(src + 8);");
+        k.line("}");
+    }
+    if (!q_post.empty()) { k.line("{"); k.s << q_post; k.line("}"); }
     if (sep) {
         k.line("if (chunk == " + std::to_string(NCH) + ") {");
         k.indent++;
-        emit_q();
-        emit_writes(true);
+            emit_writes(true);
         k.line("__syncthreads();");
         k.line("const bool nvis = krow >= 0 && krow >= lo0 && krow < hi0;");
         for (int r = 0; r < REP; r++) {
             // score of head grp·REP + r at the new row (wave r % 4), the leaf with its contraction substituted
-            k.line("if (wv == " + std::to_string(r % 4) + ") {");
+            k.line("if (wv == " + std::to_string(r % NW) + ") {");
             k.indent++;
             k.line("float dv = 0.0f;");
             k.line("for (int dd = lane; dd < " + std::to_string(HD) + "; dd += 64) dv = fmaf(q_lds[" + std::to_string(r * HD) + " + dd], knew_lds[dd], dv);");
@@ -527,7 +578,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         }
         k.line("__syncthreads();");
         // the one-position partial: m = score, scalar slots into·1, vector slots the value row
-        k.line("for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += 256) {");
+        k.line("for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += " + std::to_string(NT) + ") {");
         k.indent++;
         k.line("const int r = i / " + std::to_string(PSZ) + ", f = i % " + std::to_string(PSZ) + ";");
         k.line("const float m = stat_lds[r][0];");
@@ -545,7 +596,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     }
     // identity partial for chunks past the visible window
     k.line("if (t0 >= hi0) {");
-    k.line("  for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += 256) {");
+    k.line("  for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += " + std::to_string(NT) + ") {");
     k.line("    const int r = i / " + std::to_string(PSZ) + ", f = i % " + std::to_string(PSZ) + ";");
     k.line("    sanic_st(part + r * " + std::to_string(PSZ) + " + f, f == 0 ? " + flit(c.identity[P.max_slot]) + " : 0.0f);");
     k.line("  }");
@@ -562,13 +613,12 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     } else {
         emit_writes(false);
     }
-    emit_q();
     k.line("__syncthreads();");
     // scores
     k.line("#pragma unroll");
     k.line("for (int ps = 0; ps < " + std::to_string(NP) + "; ++ps) {");
     k.indent++;
-    k.line("const int tl = ps * 64 + tid / " + std::to_string(LPT) + ";");
+    k.line("const int tl = ps * " + std::to_string(PPP) + " + tid / " + std::to_string(LPT) + ";");
     k.line("const idx_t t = t0 + tl;");
     k.line("float dot[" + std::to_string(REP) + "];");
     k.line("#pragma unroll");
@@ -629,7 +679,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("}");
     k.line("__syncthreads();");
     // per head: max, p = exp(s − m) (0 when m = −∞), Σ p
-    k.line("for (int r = wv; r < " + std::to_string(REP) + "; r += 4) {");
+    k.line("for (int r = wv; r < " + std::to_string(REP) + "; r += " + std::to_string(NW) + ") {");
     k.indent++;
     k.line("float m = (-__builtin_huge_valf());");
     k.line("for (int i = lane; i < " + std::to_string(CH) + "; i += 64) m = fmaxf(m, p_lds[r][i]);");
@@ -652,9 +702,9 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("#pragma unroll");
     k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) o[r] = 0.0f;");
     k.line("#pragma unroll");
-    k.line("for (int sb = 0; sb < " + std::to_string(NP) + "; ++sb) {");
+    k.line("for (int sb = 0; sb < " + std::to_string(NSB) + "; ++sb) {");
     k.indent++;
-    k.line("const int tbase = tg * " + std::to_string(CH / 4) + " + sb * 16;");
+    k.line("const int tbase = tg * " + std::to_string(PG) + " + sb * 16;");
     if (vfast) {
         // the prefetched run covers the block whenever it lies inside the cache; positions past
         // the window contribute nothing (their value is masked to 0 and their probability is 0)
@@ -708,14 +758,14 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("}");
     k.line("__syncthreads();");
     // write the partial carriers: [m, scalar slots (into·ℓ), vector slots (o)]
-    k.line("for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += 256) {");
+    k.line("for (int i = tid; i < " + std::to_string(REP * PSZ) + "; i += " + std::to_string(NT) + ") {");
     k.indent++;
     k.line("const int r = i / " + std::to_string(PSZ) + ", f = i % " + std::to_string(PSZ) + ";");
     k.line("float v;");
     k.line("if (f == 0) v = stat_lds[r][0];");
     for (int s = 0; s < NS; s++)
         k.line("else if (f == " + std::to_string(1 + s) + ") v = " + flit(P.scalar_into[s]) + " * stat_lds[r][1];");
-    k.line("else { const int e = (f - " + std::to_string(1 + NS) + ") % " + std::to_string(E) + "; v = ((o_lds[0][r][e] + o_lds[1][r][e]) + o_lds[2][r][e]) + o_lds[3][r][e]; }");
+    k.line("else { const int e = (f - " + std::to_string(1 + NS) + ") % " + std::to_string(E) + "; v = o_lds[0][r][e]; for (int g = 1; g < " + std::to_string(NW) + "; ++g) v += o_lds[g][r][e]; }");
     k.line("sanic_st(part + r * " + std::to_string(PSZ) + " + f, v);");
     k.indent--;
     k.line("}");
@@ -746,36 +796,36 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     // 16-byte loads when a chunk's group partials are 16-byte aligned runs
     if ((REP * PSZ) % 4 == 0 && (NH * PSZ) % 4 == 0 && part_off % 16 == 0) {
         const int64_t Q4 = REP * PSZ / 4;                     // float4 per chunk
-        const int64_t PER = (NPART * Q4 + 255) / 256;
+        const int64_t PER = (NPART * Q4 + NT - 1) / NT;
         k.line("const float* gbase = a.scratch + " + std::to_string(part_off / 4) + " + grp * " + std::to_string(REP * PSZ) + ";");
         k.line("sanic_f32x4 gv[" + std::to_string(PER) + "];");
         k.line("#pragma unroll");
         k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j) {");
-        k.line("  const int i = tid + j * 256;");
+        k.line("  const int i = tid + j * " + std::to_string(NT) + ";");
         k.line("  const int ch = i / " + std::to_string(Q4) + ", w = i % " + std::to_string(Q4) + ";");
         k.line("  gv[j] = sanic_ld4(gbase, (unsigned)((i < " + std::to_string(NPART * Q4) + " ? ch * " + std::to_string(NH * PSZ) + " + w * 4 : 0) * 4));");
         k.line("}");
         k.line("#pragma unroll");
         k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j)");
-        k.line("  if (tid + j * 256 < " + std::to_string(NPART * Q4) + ") *(sanic_f32x4*)(g_lds + (tid + j * 256) * 4) = gv[j];");
+        k.line("  if (tid + j * " + std::to_string(NT) + " < " + std::to_string(NPART * Q4) + ") *(sanic_f32x4*)(g_lds + (tid + j * " + std::to_string(NT) + ") * 4) = gv[j];");
     } else {
-        const int64_t PER = (GP + 255) / 256;
+        const int64_t PER = (GP + NT - 1) / NT;
         k.line("float gv[" + std::to_string(PER) + "];");
         k.line("#pragma unroll");
         k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j) {");
-        k.line("  const int i = tid + j * 256;");
+        k.line("  const int i = tid + j * " + std::to_string(NT) + ";");
         k.line("  const int ch = i / " + std::to_string(REP * PSZ) + ", rem = i % " + std::to_string(REP * PSZ) + ";");
         k.line("  gv[j] = i < " + std::to_string(GP) + " ? sanic_ld(a.scratch + " + std::to_string(part_off / 4) + " + (ch * " + std::to_string(NH) + " + grp * " +
                std::to_string(REP) + ") * " + std::to_string(PSZ) + " + rem) : 0.0f;");
         k.line("}");
         k.line("#pragma unroll");
         k.line("for (int j = 0; j < " + std::to_string(PER) + "; ++j)");
-        k.line("  if (tid + j * 256 < " + std::to_string(GP) + ") g_lds[tid + j * 256] = gv[j];");
+        k.line("  if (tid + j * " + std::to_string(NT) + " < " + std::to_string(GP) + ") g_lds[tid + j * " + std::to_string(NT) + "] = gv[j];");
     }
     k.line("__syncthreads();");
     k.line("if (tid == 0) sanic_st(cnt, 0u);");
     // per head (one wave each): M and the chunk weights
-    k.line("for (int r = wv; r < " + std::to_string(REP) + "; r += 4) {");
+    k.line("for (int r = wv; r < " + std::to_string(REP) + "; r += " + std::to_string(NW) + ") {");
     k.indent++;
     k.line("float m = (-__builtin_huge_valf());");
     k.line("for (int ch = lane; ch < " + std::to_string(NPART) + "; ch += 64) m = fmaxf(m, g_lds[(ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + "]);");
@@ -788,7 +838,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.indent--;
     k.line("}");
     k.line("__syncthreads();");
-    k.line("for (int pt = tid; pt < " + std::to_string(REP * E) + "; pt += 256) {");
+    k.line("for (int pt = tid; pt < " + std::to_string(REP * E) + "; pt += " + std::to_string(NT) + ") {");
     k.indent++;
     k.line("const int r = pt / " + std::to_string(E) + ", ee = pt % " + std::to_string(E) + ";");
     for (int j = 0; j < st.rank; j++) {
@@ -839,12 +889,12 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const std::string kpart = "sanic_attn_decode_" + tag;
     std::ostringstream src;
     src << kPrelude << R.args_struct({"float* __restrict__ scratch"});
-    src << "extern \"C\" __global__ void __launch_bounds__(256) " << kpart << "(Args a) {\n" << R.entry() << k.str() << "}\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(" << NT << ") " << kpart << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     out.kernel_kind = "skeleton:attn_decode[rep " + std::to_string(REP) + "]" + (writes.empty() ? "" : "+writes" + std::to_string(writes.size())) + (sep ? "+rowwg" : "");
     out.source = src.str();
     std::vector<Arg> args = R.arg_list();
     args.push_back({Arg::SCRATCH, 0});
-    out.launches.push_back({kpart, "", dim3((unsigned)NG, (unsigned)NPART), dim3(256), 0, args});
+    out.launches.push_back({kpart, "", dim3((unsigned)NG, (unsigned)NPART), dim3((unsigned)NT), 0, args});
     return true;
 }
 
