@@ -159,7 +159,10 @@ def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
     H, hd, NH, NKV, F, V, Cap = S.hidden, S.head_dim, S.heads, S.kv_heads, S.ffn, S.vocab, S.capacity
     rep = NH // NKV
     p = Program()
-    tokens = p.input("tokens", (1,), ir.F32)
+    # the current token is step state too: the argmax's last workgroup writes the next one in
+    # place (the reference feeds `token` back into the `tokens` input, compile.rs:869-961; as a
+    # state the conversion runs inside the argmax kernel instead of as one more launch)
+    tokens = p.state("tokens", (1,), ir.F32)
     # position is step state advanced on the device at the end of each step (graph.rs:51-125
     # `state` + `update`), so back-to-back replays need no host write
     pos = p.state("position", (), ir.F32)
@@ -227,6 +230,7 @@ def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
             sched=argmax_sched or Sched(lane_stream=True, waves=4, chunk=4, split=64))
     p.pointwise("position.next", ir.map_(ir.ADD, p.node("position"), ir.const(1.0)), ir.F32,
                 grid=(), into="position")
+    p.pointwise("tokens.next", p.node("token"), ir.F32, grid=(1,), into="tokens")
     return p
 
 

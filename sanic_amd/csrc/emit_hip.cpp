@@ -818,6 +818,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     int chunk = std::max(1, st.sched.chunk);
     Renderer R(d);
     for (int t : tails) R.coherent.insert(d->stages[t].out_buffer);
+    if (!tails.empty()) R.coherent.insert(st.out_buffer);   // tails may read the merged result
     Code body;
     body.indent = 1;
     std::ostringstream src;

@@ -701,7 +701,9 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         const int64_t KQ = K / 4;
         const int KIq = (int)(KQ / 512);
         const int NSEG = (int)group.size();
-        int RBI = K >= 8192 ? 4 : 2;
+        // rows per workgroup: 4 for long rows and for very tall matrices (lm_head: fewer, fuller
+        // workgroups measured faster), else 2
+        int RBI = K >= 8192 || NTOT >= 65536 ? 4 : 2;
         if (const char* e = getenv("SANIC_GEMV_RB")) RBI = std::max(1, std::min(8, atoi(e)));
         if (paired >= 0) RBI = 2;
         if (paired >= 0) if (const char* e = getenv("SANIC_GEMV_PRB")) RBI = std::max(1, std::min(4, atoi(e)));

@@ -1,10 +1,10 @@
 """Stateful decode over the HIP backend: the `Graph::compile_for` → `instantiate` →
 `Machine::step` path (/root/reference/src/graph.rs:231-345) for the Llama-3.2 decode program.
 
-States (the K/V caches and the position) are allocated and zeroed at instantiation
-(graph.rs:297-310); one step is one hipGraph replay; the greedy token is fed back into the
-`tokens` input inside the graph (the reference's feedback binding, compile.rs:869-961), so
-decode steps launch back to back with no host round trip. Prompt tokens are written by the host
+States (the K/V caches, the position and the current token) are allocated and zeroed at
+instantiation (graph.rs:297-310); one step is one hipGraph replay; the greedy token is written
+into the `tokens` state by the argmax kernel itself (where the reference feeds `token` back into
+an input, compile.rs:869-961), so decode steps launch back to back with no host round trip. Prompt tokens are written by the host
 before each prefill step, as the reference's token-by-token prefill does
 (/root/reference/examples/llama3_2.rs:587-680).
 """
@@ -28,14 +28,13 @@ class LlamaMachine:
         self.prog = configs.llama_decode(shape, attn_sched=attn_sched)
         self.exe = dev.prepare(self.prog)
         self.bind: Dict[str, Buffer] = dict(weights)
-        self.tokens = dev.alloc(4)
-        self.bind["tokens"] = self.tokens
         for b in self.prog.buffers:
             if b.role == STATE:
                 buf = dev.alloc(b.nbytes)
                 buf.upload(bytes(b.nbytes))          # states start at zero
                 self.bind[b.name] = buf
-        self.replay = self.exe.capture(self.bind, feedback=[("token", "tokens")])
+        self.tokens = self.bind["tokens"]
+        self.replay = self.exe.capture(self.bind)
         self.logits = self.replay.buffer("logits")
         self.token = self.replay.buffer("token")
 

@@ -68,3 +68,19 @@ def test_split_fold_merges_in_last_workgroup(dev):
     for _ in range(2):
         out = exe.execute({"X": buf})["I"].read(ir.U32, 1)
         assert int(out[0]) == 77_777
+
+
+def test_capture_feedback_converts_output_into_input(dev):
+    """capture(bindings, feedback): a u32 output fed back into an f32 input inside the graph,
+    so each replay sees the previous step's output (compile.rs:869-961, RunError::Feedback on
+    mismatched volumes)."""
+    p = Program()
+    x = p.input("x", (8,), ir.F32)
+    p.pointwise("t", ir.map_(ir.ADD, x, ir.const(1.0)), ir.U32)
+    exe = dev.prepare(p)
+    xb = dev.from_values(np.arange(8, dtype=np.float64), ir.F32)
+    rp = exe.capture({"x": xb}, feedback=[("t", "x")])
+    for _ in range(3):
+        rp.step()
+    np.testing.assert_array_equal(xb.read(ir.F32, 8), np.arange(8) + 3.0)
+    np.testing.assert_array_equal(rp.buffer("t").read(ir.U32, 8), np.arange(8) + 3)
