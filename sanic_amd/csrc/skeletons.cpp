@@ -614,6 +614,39 @@ void emit_tail(Renderer& R, Code& k, const sanic_program_desc* d, const std::vec
     k.line("}");
 }
 
+// The loads an elementwise epilogue makes at the output point `gc` (a residual read, say),
+// rendered ahead of time: the epilogue is rendered once with a stand-in fold value and the
+// variables of its buffer loads are returned by node, to be substituted when the epilogue is
+// rendered for real. The loads then go out with the weight stream instead of after the
+// reduction. Empty when the tree has an in-body reduction (a node could then be read at
+// several points).
+static std::map<int, std::string> prefetch_epilogue(Renderer& R, Code& k, const sanic_program_desc* d, int epi,
+                                                    const std::vector<std::string>& gc) {
+    std::map<int, std::string> vars;
+    std::vector<int> stack{epi};
+    while (!stack.empty()) {
+        int ni = stack.back();
+        stack.pop_back();
+        const sanic_node& n = d->nodes[ni];
+        if (n.kind == SANIC_NODE_REDUCE || n.kind == SANIC_NODE_GATHER) return vars;
+        for (int j = 0; j < n.n_in; j++) stack.push_back(n.in[j]);
+    }
+    const std::string saved = R.fold_var;
+    R.fold_var = "0.0f";
+    R.memo.emplace_back();
+    Code tmp;
+    tmp.indent = k.indent;
+    R.value(tmp, epi, gc);
+    for (auto& kv : R.memo.back()) {
+        int node = atoi(kv.first.c_str());
+        if (d->nodes[node].kind == SANIC_NODE_INPUT) vars[node] = kv.second;
+    }
+    R.memo.pop_back();
+    R.fold_var = saved;
+    k.s << tmp.str();
+    return vars;
+}
+
 bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std::vector<LoweredStage>& out) {
     GemvPlan P0;
     if (!gemv_plan(d, si, P0)) return false;
@@ -793,6 +826,14 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
                 k.s << l1.str();
             }
         }
+        // epilogue operands of each row, requested behind the weights (single-segment launches)
+        std::vector<std::map<int, std::string>> epi_pre(RB);
+        if (group.size() == 1 && paired < 0 && st0.epilogue >= 0 && !getenv("SANIC_GEMV_NO_EPI_PREFETCH"))
+            for (int q = 0; q < RB; q++) {
+                std::vector<std::string> gc(st0.rank, "0");
+                gc[P0.ndim] = "nn" + std::to_string(q);
+                epi_pre[q] = prefetch_epilogue(R, k, d, st0.epilogue, gc);
+            }
         k.s << adc.str() << wdc.str();
         for (int r = 0; r < SR; r++) k.line("float rpart" + std::to_string(r) + " = 0.0f;");
         for (int q = 0; q < RB; q++)
@@ -819,6 +860,10 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
                         k.line(a + " = fmaf(af" + std::to_string(cs) + "_" + ij + ", " + wvals[q][i][j] + ", " + a + ");");
                     }
             }
+        // keep the prefetched epilogue operands where they were requested (not sunk into the
+        // finishing thread's branch)
+        for (auto& m : epi_pre)
+            for (auto& kv : m) k.line("asm volatile(\"\" :: \"v\"(" + kv.second + "));");
         // wave partials -> LDS -> one thread per row finishes it
         std::vector<std::string> parts;
         for (int q = 0; q < RB; q++)
@@ -843,7 +888,9 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
             c.line(arr + "};");
             for (int r = 0; r < SR; r++) c.line("const float racc" + std::to_string(r) + " = " + sum4(RB * SC + r) + ";");
             R.memo.emplace_back();
+            for (auto& kv : epi_pre[q]) R.subst[kv.first] = kv.second;
             std::string v = gemv_finish(R, c, d, group[g], !tails.empty());
+            for (auto& kv : epi_pre[q]) R.subst.erase(kv.first);
             R.memo.pop_back();
             return v;
         };
