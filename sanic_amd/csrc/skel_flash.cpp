@@ -339,12 +339,13 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
            "  return __builtin_bit_cast(unsigned, __builtin_convertvector((sanic_f32x2){x, y}, sanic_bf16x2));\n}\n";
     // max across the 4 lane groups of a query column (lanes l, l^16, l^32, l^48): gfx950
     // permlane swaps, no LDS round trip
-    // raw hardware max (scores from the matrix cores never carry signaling NaNs, so the
-    // operand quieting fmaxf adds in IEEE mode is pure overhead here)
+    // compiler-visible maxima: the compiler forms v_max3_f32 itself and, unlike for inline asm
+    // (which it cannot see into), inserts the wait states a VALU read of a fresh MFMA result
+    // needs; an asm max placed right after the MFMA read stale accumulator registers
     src << "__device__ __forceinline__ float hmax(float a, float b) {\n"
-           "  float r; asm(\"v_max_f32 %0, %1, %2\" : \"=v\"(r) : \"v\"(a), \"v\"(b)); return r;\n}\n";
+           "  return __builtin_fmaxf(a, b);\n}\n";
     src << "__device__ __forceinline__ float hmax3(float a, float b, float c) {\n"
-           "  float r; asm(\"v_max3_f32 %0, %1, %2, %3\" : \"=v\"(r) : \"v\"(a), \"v\"(b), \"v\"(c)); return r;\n}\n";
+           "  return __builtin_fmaxf(__builtin_fmaxf(a, b), c);\n}\n";
     src << "__device__ __forceinline__ float wave_max_x4(float v) {\n"
            "  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);\n"
            "  v = hmax(__uint_as_float(r32[0]), __uint_as_float(r32[1]));\n"
@@ -479,8 +480,8 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // scores one query tile at a time (the second tile's accumulators reuse the first's
     // registers once its softmax is done; the K fragments are re-read from LDS)
     k.line("f32x4 s[4][2];");
-    // online softmax per query column (lane-local; the max reduces across the 4 lane groups)
     k.line("sanic_u32x4 pw[2][2];");
+    // online softmax per query column (lane-local; the max reduces across the 4 lane groups)
     k.line("#pragma unroll");
     k.line("for (int qt = 0; qt < 2; ++qt) {");
     k.indent++;
