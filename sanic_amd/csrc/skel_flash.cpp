@@ -368,8 +368,10 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     const std::string kname = "sanic_flash_h" + std::to_string(NH) + "_s" + std::to_string(NQ) + "_t" + std::to_string(T);
     Code k;
     k.indent = 1;
-    const int KS = 72;      // LDS row stride (bf16) of the K tile: 64 + 8 padding
-    const int VS = 72;      // LDS row stride of the V^T tile
+    int KS = 72;      // LDS row stride (bf16) of the K tile: 64 + 8 padding
+    int VS = 72;      // LDS row stride of the V tile
+    if (const char* e = getenv("SANIC_FLASH_KS")) KS = std::max(64, atoi(e) / 8 * 8);
+    if (const char* e = getenv("SANIC_FLASH_VS")) VS = std::max(64, atoi(e) / 8 * 8);
     k.line("__shared__ unsigned short k_lds[2][64 * " + std::to_string(KS) + "];");
     k.line("__shared__ unsigned short v_lds[2][64 * " + std::to_string(VS) + "];");
     k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
