@@ -277,6 +277,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true", help="run only the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--tune", action="store_true",
+                    help="run the measured tiling tuner (SANIC_TUNE) on the decode program first and "
+                         "bench the tuned program (tuning is outside the timed region)")
     ap.add_argument("--config", default=None, help="measure a secondary configuration instead: " + ", ".join(CONFIGS))
     args = ap.parse_args()
     if args.pmc_probe:
@@ -304,7 +307,24 @@ def main():
     dev = HipDevice(0)
     t0 = time.perf_counter()
     weights, keep = device_weights(dev, shape)
-    m = LlamaMachine(dev, weights, shape)
+    tuned = None
+    if args.tune:
+        from sanic_amd import tune as tuner
+        prog = configs.llama_decode(shape)
+        # zeroed bindings, the decode position rewound to the end of the prompt before every
+        # timing: every candidate is judged on the same steps the bench times
+        bind = tuner.zero_bindings(dev, prog)
+        import struct
+        rep = tuner.tune(dev, prog, bind, reset=lambda: bind["position"].upload(struct.pack("<f", float(PROMPT))))
+        for kern, v, base, cand in rep.trials:
+            log(f"tune {kern} variant {v}: {cand * 1e6:.1f} us vs adjacent {base * 1e6:.1f} us")
+        log(f"tune: analytic {rep.baseline_s * 1e6:.1f} us, tuned {rep.tuned_s * 1e6:.1f} us, "
+            f"shipped {rep.shipped} {rep.choices}")
+        tuned = {"shipped": rep.shipped, "choices": rep.choices,
+                 "analytic_us": rep.baseline_s * 1e6, "tuned_us": rep.tuned_s * 1e6}
+        m = LlamaMachine(dev, weights, shape, variants=rep.variants)
+    else:
+        m = LlamaMachine(dev, weights, shape)
     log(f"prepared in {time.perf_counter() - t0:.1f}s")
 
     import numpy as np
@@ -348,6 +368,8 @@ def main():
         "gpu_event_seconds": gpu_s, "wall_seconds": wall,
         "prefill_token_by_token_tok_s": PROMPT / prefill_s,
     }
+    if tuned is not None:
+        out["tuned"] = tuned
     print(json.dumps(out))
 
 

@@ -161,11 +161,15 @@ typedef struct sanic_carrier {
  *   split:       workgroups that fold disjoint slices of the stream; their partial carriers are
  *                merged by the carrier's own combine in a second pass (the split-K /
  *                Flash-Decoding combine; oracle = interp.rs:555-643 run_carrier_split)      */
+/* variant:     tiling variant of the hand-written kernel that lowers the stage (0 = the
+ *              analytic choice): the measured tuner's handle, as the reference's SANIC_TUNE swaps
+ *              FoldSched candidates (compile.rs:1348-1630). Generic folds ignore it.       */
 typedef struct sanic_sched {
     int32_t lane_stream;
     int32_t waves;
     int32_t chunk;
     int32_t split;
+    int32_t variant;
 } sanic_sched;
 
 /* Stage kinds (/root/reference/src/partition.rs:44-98). */
@@ -298,6 +302,12 @@ int sanic_hip_sync(sanic_hip_device* dev);
 int sanic_hip_emit_source(const sanic_program_desc* desc, int stage, char* kind, size_t kind_cap,
                           char* source, size_t source_cap);
 int sanic_hip_precompile(const sanic_program_desc* desc);
+/* Number of tiling variants (sanic_sched.variant values) the kernel lowering `stage` offers
+ * (1 when it has none; 0 for a stage folded into another stage's launch): the measured
+ * tuner's candidate space (the reference prices FoldSched candidates, plan.rs:604-850, and
+ * SANIC_TUNE times them in the full step, compile.rs:1348-1630). With stage = -1, `count`
+ * holds n_stages entries and receives every stage's count from one lowering. */
+int sanic_hip_stage_variants(const sanic_program_desc* desc, int stage, int* count);
 size_t sanic_hip_abi_sizeof(const char* record_name);
 
 #ifdef __cplusplus

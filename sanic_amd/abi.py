@@ -36,7 +36,7 @@ CARRIER_DT = np.dtype([
 ], align=True)
 
 SCHED_DT = np.dtype([("lane_stream", "<i4"), ("waves", "<i4"), ("chunk", "<i4"),
-                     ("split", "<i4")], align=True)
+                     ("split", "<i4"), ("variant", "<i4")], align=True)
 
 STAGE_DT = np.dtype([
     ("kind", "<i4"), ("out_buffer", "<i4"), ("out_dtype", "<i4"), ("rank", "<i4"),
@@ -102,6 +102,7 @@ SIGNATURES = {
     "sanic_hip_sync": (I, [VP]),
     "sanic_hip_abi_sizeof": (SZ, [ctypes.c_char_p]),
     "sanic_hip_precompile": (I, [ctypes.POINTER(ProgramDesc)]),
+    "sanic_hip_stage_variants": (I, [ctypes.POINTER(ProgramDesc), I, ctypes.POINTER(ctypes.c_int)]),
     "sanic_hip_emit_source": (I, [ctypes.POINTER(ProgramDesc), I, ctypes.c_char_p, SZ,
                                   ctypes.c_char_p, SZ]),
 }

@@ -67,6 +67,13 @@ def precompile_all() -> None:
     for p in (rmsnorm_projection(kmajor=False), rmsnorm_projection(kmajor=True), int4_matmul(),
               decode_attention(), llama_decode(), flash_prefill(), flash_prefill(window=1024)):
         p.precompile()
+    # every tiling variant the measured tuner may try (each stage takes variant v when it has
+    # more than v; identical sources compile once)
+    for p in (llama_decode(), decode_attention(), rmsnorm_projection(kmajor=False),
+              flash_prefill(), flash_prefill(window=1024), flash_prefill(4, 2, 256), flash_prefill(4, 2, 256, window=64)):
+        counts = p.stage_variants(-1)
+        for v in range(1, max(counts) if counts else 1):
+            p.with_variants({i: v for i, n in enumerate(counts) if n > v}).precompile()
 
 
 def rmsnorm_projection(M: int = 1, K: int = 2048, N: int = 8192, eps: float = 1e-5,

@@ -55,6 +55,7 @@ struct Launch {
 struct LoweredStage {
     std::string kernel_kind;   // "skeleton:<name>" or "fold:<scalar|coop|split>" or "pointwise"
     std::string source;        // generated HIP source
+    int variants = 1;          // tiling variants the lowering offers (sanic_sched.variant)
     std::vector<Launch> launches;
 };
 

@@ -351,7 +351,10 @@ void Code::line(const std::string& l) {
 std::string Renderer::param(int buffer) {
     auto it = buf_param.find(buffer);
     if (it != buf_param.end()) return it->second;
-    std::string name = "a.b" + std::to_string(buffer);
+    // parameters are named by position, not by program buffer: stages that differ only in which
+    // buffers they read (the layers of a model) render to the same source and share one code
+    // object (the reference dedups isomorphic kernels, emit_metal.rs:1283-1327)
+    std::string name = "a.b" + std::to_string(bufs.size());
     buf_param[buffer] = name;
     bufs.push_back(buffer);
     return name;
@@ -362,9 +365,9 @@ std::string Renderer::fresh(const char* p) { return std::string(p) + std::to_str
 std::string Renderer::args_struct(const std::vector<std::string>& extra) const {
     std::ostringstream o;
     o << "struct Args {\n";
-    for (int b : bufs) {
-        int dt = d->buffers[b].dtype;
-        o << "  " << ctype_of(dt) << "* __restrict__ b" << b << ";\n";
+    for (size_t i = 0; i < bufs.size(); i++) {
+        int dt = d->buffers[bufs[i]].dtype;
+        o << "  " << ctype_of(dt) << "* __restrict__ b" << i << ";\n";
     }
     for (auto& e : extra) o << "  " << e << ";\n";
     o << "};\n";

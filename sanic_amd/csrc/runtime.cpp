@@ -551,6 +551,20 @@ int sanic_hip_emit_source(const sanic_program_desc* desc, int stage, char* kind,
     });
 }
 
+int sanic_hip_stage_variants(const sanic_program_desc* desc, int stage, int* count) {
+    return guarded([&] {
+        Lowered low = lower_program(desc);
+        if (!count) fail(SANIC_ERR_ARG, "null count");
+        auto one = [&](int i) { return low.stages[i].launches.empty() ? 0 : low.stages[i].variants; };
+        if (stage == -1) {
+            for (int i = 0; i < (int)low.stages.size(); i++) count[i] = one(i);
+            return;
+        }
+        if (stage < 0 || stage >= (int)low.stages.size()) fail(SANIC_ERR_ARG, "stage out of range");
+        *count = one(stage);
+    });
+}
+
 int sanic_hip_precompile(const sanic_program_desc* desc) {
     return guarded([&] {
         sanic_hip_exe exe;

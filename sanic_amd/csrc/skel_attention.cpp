@@ -330,12 +330,17 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const int PSZ = 1 + NS + NV * (int)E;         // floats per (chunk, head) partial
     // stream positions per workgroup: 128 (measured best at ~2k positions against 64 and 256),
     // doubled until one group's partials fit the merging workgroup's LDS
-    // threads per workgroup: 1024 (16 waves, four per SIMD, so the dependent LDS/shuffle phases
-    // of one wave hide behind the others'), over 256-position chunks
-    int NT = 1024;
+    // threads per workgroup: 512 (8 waves, two per SIMD, so the dependent LDS/shuffle phases of
+    // one wave hide behind the other's), over 128-position chunks: measured in the full decode
+    // step against 1024 threads × 256 positions (the measured tuner's pick, 3% per step)
+    // tiling variants for the measured tuner: (threads, positions per chunk; 0 = the rule below)
+    static const int kVariants[][2] = {{512, 0}, {1024, 0}, {1024, 512}, {512, 256}, {256, 0}};
+    const int nvar = (int)(sizeof kVariants / sizeof *kVariants);
+    const int var = st.sched.variant >= 0 && st.sched.variant < nvar ? st.sched.variant : 0;
+    int NT = kVariants[var][0];
     if (const char* e = getenv("SANIC_ATTN_NT")) NT = atoi(e) >= 1024 ? 1024 : atoi(e) >= 512 ? 512 : 256;
     const int NW = NT / 64;
-    int CH = NT / 4;
+    int CH = kVariants[var][1] ? kVariants[var][1] : NT / 4;
     while (CH < 1024 && ((T + CH - 1) / CH) * REP * PSZ * 4 > 40 * 1024) CH *= 2;
     if (const char* e = getenv("SANIC_ATTN_CH")) CH = std::max(NT / 4, std::min(1024, atoi(e) / (NT / 4) * (NT / 4)));
     const int64_t NCH = (T + CH - 1) / CH;
@@ -361,7 +366,10 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         sep = rp[0] == rp[1];
     }
     const int64_t NPART = NCH + (sep ? 1 : 0);   // partial carriers per KV group
-    int64_t part_off = scratch;
+    // scratch offsets in the source are relative to this stage's base (passed as the argument),
+    // so the same stage in every layer renders to the same source
+    const int64_t sbase = scratch;
+    const int64_t part_off = 0;
     scratch += ((NPART * NH * PSZ * 4 + 255) / 256) * 256;
     Renderer R(d);
     Code k;
@@ -776,7 +784,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     // applied to all chunks at once): M = max_c m_c, w_c = [−∞ < m_c]·exp(m_c − M), every
     // ExpShifted slot = Σ_c w_c·x_c. This is the pairwise combine of run_carrier_split
     // (interp.rs:555-643) regrouped — no chain of NCH dependent steps.
-    int64_t counter_off = scratch;
+    const int64_t counter_off = scratch - sbase;
     scratch += ((NG * 4 + 255) / 256) * 256;
     const int64_t GP = NPART * REP * PSZ;       // floats of one group's partials
     if (GP * 4 > 64 * 1024) return false;
@@ -892,8 +900,9 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     src << "extern \"C\" __global__ void __launch_bounds__(" << NT << ") " << kpart << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     out.kernel_kind = "skeleton:attn_decode[rep " + std::to_string(REP) + "]" + (writes.empty() ? "" : "+writes" + std::to_string(writes.size())) + (sep ? "+rowwg" : "");
     out.source = src.str();
+    out.variants = nvar;
     std::vector<Arg> args = R.arg_list();
-    args.push_back({Arg::SCRATCH, 0});
+    args.push_back({Arg::SCRATCH, sbase});
     out.launches.push_back({kpart, "", dim3((unsigned)NG, (unsigned)NPART), dim3((unsigned)NT), 0, args});
     return true;
 }

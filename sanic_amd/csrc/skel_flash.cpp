@@ -641,11 +641,13 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
 
     // three waves per SIMD: the softmax of one wave overlaps the MFMAs of the others (the
     // register cap costs a few spilled values outside the inner loop)
-    int occ = 3;
+    // tiling variants for the measured tuner: workgroups per CU {3, 2}
+    int occ = d->stages[si].sched.variant == 1 ? 2 : 3;
     if (const char* e = getenv("SANIC_FLASH_OCC")) occ = std::max(1, std::min(4, atoi(e)));
     src << "extern \"C\" __global__ void __launch_bounds__(256, " << occ << ") " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     out.kernel_kind = "skeleton:flash_prefill[rep " + std::to_string(P.rep) + "]";
     out.source = src.str();
+    out.variants = 2;
     out.launches.push_back({kname, "", dim3((unsigned)(NH * NQB)), dim3(256), 0, R.arg_list()});
     return true;
 }

@@ -737,8 +737,13 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         // rows per workgroup: 4 for long rows and for very tall matrices (lm_head: fewer, fuller
         // workgroups measured faster), else 2
         int RBI = K >= 8192 || NTOT >= 65536 ? 4 : 2;
+        // tiling variants for the measured tuner: rows per workgroup {rule, 1, 2, 4} ({2, 1}
+        // for a paired launch, whose workgroup holds row i of every segment)
+        const int gvar = d->stages[si].sched.variant;
+        const int nvar = paired >= 0 ? 2 : 4;
+        if (gvar > 0 && gvar < nvar) RBI = paired >= 0 ? 1 : (1 << (gvar - 1));
         if (const char* e = getenv("SANIC_GEMV_RB")) RBI = std::max(1, std::min(8, atoi(e)));
-        if (paired >= 0) RBI = 2;
+        if (paired >= 0 && !(gvar > 0 && gvar < nvar)) RBI = 2;
         if (paired >= 0) if (const char* e = getenv("SANIC_GEMV_PRB")) RBI = std::max(1, std::min(4, atoi(e)));
         const int RB = paired >= 0 ? RBI * NSEG : RBI;           // rows per workgroup
         const int64_t UNITS = paired >= 0 ? P0.N : NTOT;
@@ -948,7 +953,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
             }
         }
         if (!tails.empty())
-            emit_tail(R, k, d, tails, "(unsigned*)((char*)a.scratch + " + std::to_string(counter_off) + ")", "gridDim.x");
+            emit_tail(R, k, d, tails, "(unsigned*)a.scratch", "gridDim.x");
         const std::string kname = "sanic_gemv_" + std::to_string(NTOT) + "x" + std::to_string(K);
         std::ostringstream src;
         src << kPrelude << R.args_struct(tails.empty() ? std::vector<std::string>{} : std::vector<std::string>{"float* __restrict__ scratch"})
@@ -957,8 +962,9 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         L.kernel_kind = "skeleton:gemv" + std::string(group.size() > 1 ? "[batched " + std::to_string(group.size()) + "]" : "") +
                         (paired >= 0 ? "+paired" : "") + (tails.empty() ? "" : "+tail" + std::to_string(tails.size()));
         L.source = src.str();
+        L.variants = nvar;
         std::vector<Arg> args = R.arg_list();
-        if (!tails.empty()) args.push_back({Arg::SCRATCH, 0});
+        if (!tails.empty()) args.push_back({Arg::SCRATCH, counter_off});   // the tail counter: relative offset 0
         L.launches.push_back({kname, "", dim3((unsigned)nblocks), dim3(256), 0, args});
         out.push_back(std::move(L));
         for (size_t g = 1; g < group.size(); g++) {
@@ -1193,7 +1199,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
     k.indent--;
     k.line("}");
     if (!tails.empty())
-        emit_tail(R, k, d, tails, "(unsigned*)((char*)a.scratch + " + std::to_string(counter_off) + ")", "gridDim.x");
+        emit_tail(R, k, d, tails, "(unsigned*)a.scratch", "gridDim.x");
 
     // kernel names carry the shape so profiles tell the launches apart
     const std::string kname = "sanic_gemv_" + std::to_string(NTOT) + "x" + std::to_string(K);
@@ -1207,7 +1213,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
     L.source = src.str();
     uint32_t lds = (uint32_t)((SC * K + 4 * std::max(SR, 1)) * 4);
     std::vector<Arg> args = R.arg_list();
-    if (!tails.empty()) args.push_back({Arg::SCRATCH, 0});
+    if (!tails.empty()) args.push_back({Arg::SCRATCH, counter_off});   // the tail counter: relative offset 0
     L.launches.push_back({kname, "", dim3((unsigned)blocks), dim3(256), lds, args});
     out.push_back(std::move(L));
     for (size_t g = 1; g < group.size(); g++) {

@@ -22,10 +22,15 @@ from .program import STATE
 
 class LlamaMachine:
     def __init__(self, dev: HipDevice, weights: Dict[str, Buffer],
-                 shape: configs.LlamaShape = configs.LLAMA_1B, attn_sched=None):
+                 shape: configs.LlamaShape = configs.LLAMA_1B, attn_sched=None,
+                 variants: Optional[Dict[int, int]] = None):
+        """`variants` (stage -> tiling variant) is what the measured tuner ships
+        (`sanic_amd.tune`); none = the analytic choice of every kernel."""
         self.dev = dev
         self.shape = shape
         self.prog = configs.llama_decode(shape, attn_sched=attn_sched)
+        if variants:
+            self.prog = self.prog.with_variants(variants)
         self.exe = dev.prepare(self.prog)
         self.bind: Dict[str, Buffer] = dict(weights)
         for b in self.prog.buffers:

@@ -30,6 +30,7 @@ class Sched:
     waves: int = 1
     chunk: int = 1
     split: int = 1
+    variant: int = 0          # tiling variant of the kernel that lowers the stage (the tuner's)
 
 
 @dataclass
@@ -183,6 +184,7 @@ class Program:
                 r["sched"]["waves"] = s.sched.waves
                 r["sched"]["chunk"] = s.sched.chunk
                 r["sched"]["split"] = s.sched.split
+                r["sched"]["variant"] = s.sched.variant
             else:
                 r["value"] = nt.add(s.value)
                 if s.where is not None:
@@ -211,6 +213,26 @@ class Program:
         src = ctypes.create_string_buffer(cap)
         abi.check(abi.lib().sanic_hip_emit_source(ctypes.byref(desc), stage, kind, 256, src, cap))
         return kind.value.decode(), src.value.decode()
+
+    def stage_variants(self, stage: int = -1):
+        """Tiling variants the kernel lowering `stage` offers (0: folded into another launch);
+        with stage = -1 the list for every stage, from one lowering."""
+        desc, keep = self.pack()
+        n = (ctypes.c_int * max(1, len(self.stages)))()
+        abi.check(abi.lib().sanic_hip_stage_variants(ctypes.byref(desc), stage, n))
+        return list(n[:len(self.stages)]) if stage == -1 else n[0]
+
+    def with_variants(self, variants: Dict[int, int]) -> "Program":
+        """A copy whose stages carry the given tiling variants (stage index -> variant)."""
+        import copy as _copy
+        import dataclasses
+        p = _copy.copy(self)
+        p.stages = list(self.stages)
+        for i, v in variants.items():
+            st = _copy.copy(p.stages[i])
+            st.sched = dataclasses.replace(st.sched or Sched(), variant=int(v))
+            p.stages[i] = st
+        return p
 
     def precompile(self):
         desc, keep = self.pack()
