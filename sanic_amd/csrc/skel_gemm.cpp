@@ -18,6 +18,8 @@
 #include <functional>
 #include <set>
 
+#include <regex>
+
 #include "emit.h"
 #include "skeletons.h"
 
@@ -165,7 +167,8 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     const sanic_stage& st = d->stages[si];
     const sanic_carrier& c = st.carrier;
     const int64_t M = P.M, N = P.N, K = P.K;
-    const int BM = M % 128 == 0 ? 128 : 64;
+    int BM = M % 128 == 0 ? 128 : 64;
+    if (const char* e = getenv("SANIC_GEMM_BM")) BM = atoi(e) <= 64 && M % 64 == 0 ? 64 : BM;
     int BN = 128;
     while (BN > 32 && (M / BM) * (N / BN) < 256) BN /= 2;
     if (const char* e = getenv("SANIC_GEMM_BN")) BN = std::max(32, std::min(128, atoi(e)));
@@ -173,7 +176,9 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     const int WM = BM / 2, WN = BN / 2;       // per-wave tile
     const int MT = WM / 16, NT = WN / 16;
     const int SR = (int)P.rslots.size();
-    const int AS = 64 + 8, BS = 64 + 8;       // LDS row strides (bf16)
+    int AS = 64 + 8;                          // LDS row strides (bf16)
+    const int BS = 64 + 8;
+    if (const char* e = getenv("SANIC_GEMM_AS")) AS = std::max(64, atoi(e) / 8 * 8);
     // An operand that is not a bf16 input as stored (x·g, dequantized weights) goes to the MFMA
     // as hi + lo bf16 pair (hi = rn(v), lo = rn(v − hi): 16 significant bits, exact for the
     // product of two bf16 values), so products match an f32 evaluation; one extra MFMA each.
@@ -227,7 +232,8 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         render_weight_run(d, st.leaf[P.w], cwt, {K, N}, l1, d1, "kk", "n0", "_p", tb, td, tok, tc, tr, false);
         bkn = tok && tc;
     }
-    const int BNS = BN + 8;                   // [k][n] B tile row stride (bf16)
+    int BNS = BN + 8;                         // [k][n] B tile row stride (bf16)
+    if (const char* e = getenv("SANIC_GEMM_BPAD")) BNS = BN + std::max(0, atoi(e) / 4 * 4);
     // row leaves vector forms over vars {0: m, 1: k}
     std::vector<std::vector<Sym>> crow;
     for (int l : P.rows) {
@@ -524,6 +530,76 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     k.indent--;
     k.line("}");
     k.line("__syncthreads();");
+    // Loads run two tiles ahead of the MFMAs: one workgroup per CU leaves a single wave per SIMD,
+    // so a tile's global loads (≈2 µs under load) must be in flight for two tiles' MFMAs, not
+    // one. Two register sets alternate in a loop unrolled by two; a set's loaded values are
+    // plain variables declared before the loop (the loads' address temporaries stay scoped).
+    const bool deep = NKT % 2 == 0 && NKT >= 4 && !getenv("SANIC_GEMM_SHALLOW");
+    if (deep) {
+        auto persistent = [&](const std::string& sfx, Code& decl) {
+            Code tmp;
+            tmp.indent = k.indent + 1;
+            emit_loads(tmp, "(idx_t)0", sfx);
+            static const std::regex re(R"(const (sanic_u32x4|float) (\w+) = )");
+            std::string t = tmp.str();
+            std::set<std::string> seen;
+            for (auto it = std::sregex_iterator(t.begin(), t.end(), re); it != std::sregex_iterator(); ++it) {
+                const std::string name = (*it)[2];
+                if (name.size() > sfx.size() && name.compare(name.size() - sfx.size(), sfx.size(), sfx) == 0 &&
+                    (name.rfind("pah", 0) == 0 || name.rfind("pal", 0) == 0 || name.rfind("rb", 0) == 0 ||
+                     name.rfind("rl", 0) == 0 || name.rfind("ra", 0) == 0) && name.rfind("rbh", 0) != 0 &&
+                    name.rfind("rbl", 0) != 0 && !seen.count(name)) {
+                    seen.insert(name);
+                    decl.line(std::string((*it)[1]) + " " + name + ";");
+                }
+            }
+            return seen;
+        };
+        // loads into a set: address temporaries in a block, the values assigned to the set
+        auto load_into = [&](const std::string& kt0, const std::string& sfx, const std::set<std::string>& names) {
+            Code tmp;
+            tmp.indent = k.indent + 1;
+            emit_loads(tmp, kt0, sfx);
+            std::string t = tmp.str();
+            for (auto& n : names) {
+                for (const char* ty : {"const sanic_u32x4 ", "const float "}) {
+                    const std::string from = std::string(ty) + n + " = ";
+                    size_t pos = t.find(from);
+                    if (pos != std::string::npos) t.replace(pos, from.size(), n + " = ");
+                }
+            }
+            k.line("{");
+            k.s << t;
+            k.line("}");
+            // keep the requests ahead of this step's MFMAs (the scheduler would sink them)
+            k.line("__builtin_amdgcn_sched_barrier(0);");
+        };
+        Code decl;
+        decl.indent = k.indent;
+        auto names_p = persistent("_p", decl);
+        auto names_q = persistent("_q", decl);
+        k.s << decl.str();
+        load_into("(idx_t)64", "_p", names_p);                      // tile 1
+        const std::string N2 = std::to_string(NKT);
+        k.line("for (idx_t kt = 0; kt < " + N2 + "; kt += 2) {");
+        k.indent++;
+        // even step: set p holds tile kt+1; tile kt+2 → set q
+        load_into("(((kt + 2) % " + N2 + ") * 64)", "_q", names_q);
+        emit_mfma(k, "0");
+        emit_stores(k, "1", "_p");
+        k.line("__syncthreads();");
+        // odd step: set q holds tile kt+2; tile kt+3 → set p
+        load_into("(((kt + 3) % " + N2 + ") * 64)", "_p", names_p);
+        emit_mfma(k, "1");
+        k.line("if (kt + 2 < " + N2 + ") {");
+        k.indent++;
+        emit_stores(k, "0", "_q");
+        k.indent--;
+        k.line("}");
+        k.line("__syncthreads();");
+        k.indent--;
+        k.line("}");
+    } else {
     k.line("for (idx_t kt = 0; kt < " + std::to_string(NKT) + "; ++kt) {");
     k.indent++;
     k.line("const int buf = (int)(kt & 1);");
@@ -539,6 +615,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     k.line("__syncthreads();");
     k.indent--;
     k.line("}");
+    }
     // row slots: sum the TPR partial rows, publish per row
     if (SR && pre) {
         k.line("for (int i = tid; i < " + std::to_string(BM * SR) + "; i += 256) rs_lds[i] = ((const float*)((const char*)a.scratch + " + std::to_string(rs_off) +
