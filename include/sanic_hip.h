@@ -89,11 +89,13 @@ enum { SANIC_MON_ADD = 0, SANIC_MON_MUL, SANIC_MON_MAX, SANIC_MON_MIN, SANIC_MON
  *               pairs; out of range reads 0 when padded (interp.rs `Reindex` arm)
  *   FOLD        placeholder for the enclosing fused stage's projected fold value at the
  *               stage's grid coordinate (used only inside an epilogue tree; shape = grid)
+ *   SCAN        in[0] = src, dim, op = monoid; shape = src shape; the inclusive prefix fold
+ *               along `dim` (interp.rs `eval_scan`, ir.rs `scan`)
  * ------------------------------------------------------------------------------------------- */
 enum {
     SANIC_NODE_INPUT = 0, SANIC_NODE_CONST, SANIC_NODE_IOTA, SANIC_NODE_COORDINATE,
     SANIC_NODE_MAP, SANIC_NODE_REDUCE, SANIC_NODE_GATHER, SANIC_NODE_VIEW, SANIC_NODE_REINDEX,
-    SANIC_NODE_FOLD
+    SANIC_NODE_FOLD, SANIC_NODE_SCAN
 };
 
 #define SANIC_MAX_RANK 8

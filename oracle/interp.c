@@ -221,6 +221,21 @@ static const double* eval_node(ctx_t* cx, int idx) {
         }
         break;
     }
+    case SANIC_NODE_SCAN: {
+        /* interp.rs eval_scan: the prefix fold up to and including this coordinate */
+        const double* src = eval_node(cx, n->in[0]);
+        for (int64_t i = 0; i < vol; i++) {
+            unflatten(i, n->shape, n->rank, c);
+            for (int j = 0; j < n->rank; j++) s[j] = c[j];
+            double acc = oracle_monoid_identity(n->op);
+            for (int64_t r = 0; r <= c[n->dim]; r++) {
+                s[n->dim] = r;
+                acc = oracle_monoid_combine(n->op, acc, src[flatten_at(s, n->shape, n->rank)]);
+            }
+            out[i] = acc;
+        }
+        break;
+    }
     case SANIC_NODE_GATHER: {
         const sanic_node* m = &cx->d->nodes[n->in[0]];
         const sanic_node* ix = &cx->d->nodes[n->in[1]];

@@ -92,6 +92,14 @@ static void check_node(const sanic_program_desc* d, int i) {
         if (n.op < 0 || n.op > SANIC_MON_LSE) bad("reduce monoid");
         break;
     }
+    case SANIC_NODE_SCAN: {
+        const sanic_node& c = child(0);
+        if (n.n_in != 1 || n.dim < 0 || n.dim >= c.rank || n.rank != c.rank) bad("scan shape");
+        for (int j = 0; j < c.rank; j++)
+            if (c.shape[j] != n.shape[j]) bad("scan shape");
+        if (n.op < 0 || n.op > SANIC_MON_LSE) bad("scan monoid");
+        break;
+    }
     case SANIC_NODE_GATHER: {
         const sanic_node& s = child(0);
         const sanic_node& x = child(1);
@@ -453,6 +461,24 @@ std::string Renderer::value(Code& code, int node, const std::vector<std::string>
         }
         out = fresh("m");
         code.line("const float " + out + " = " + map_expr(n.op, a[0], a[1], a[2]) + ";");
+        break;
+    }
+    case SANIC_NODE_SCAN: {
+        // each output point folds its own prefix (codegen.rs Scan arm): parallel across points,
+        // serial within one; inclusive of the point's own position
+        out = fresh("r");
+        std::string r = fresh("i");
+        code.line("float " + out + " = " + flit(monoid_identity(n.op)) + ";");
+        code.line("for (idx_t " + r + " = 0; " + r + " <= (idx_t)(" + c[n.dim] + "); ++" + r + ") {");
+        code.indent++;
+        memo.emplace_back();
+        std::vector<std::string> cc(c);
+        cc[n.dim] = r;
+        std::string v = value(code, n.in[0], cc);
+        code.line(out + " = " + monoid_combine(n.op, out, v) + ";");
+        memo.pop_back();
+        code.indent--;
+        code.line("}");
         break;
     }
     case SANIC_NODE_REDUCE: {

@@ -64,7 +64,7 @@ bool expr_is_const(const sanic_program_desc* d, int e, double& v) {
 
 bool contains_reduce(const sanic_program_desc* d, int node) {
     const sanic_node& n = d->nodes[node];
-    if (n.kind == SANIC_NODE_REDUCE) return true;
+    if (n.kind == SANIC_NODE_REDUCE || n.kind == SANIC_NODE_SCAN) return true;
     for (int k = 0; k < n.n_in; k++) if (contains_reduce(d, n.in[k])) return true;
     return false;
 }

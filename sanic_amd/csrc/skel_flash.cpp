@@ -81,7 +81,7 @@ bool find_flash_dot(const sanic_program_desc* d, int node, const std::vector<Sym
             std::vector<int> st{n.in[k]};
             while (!st.empty()) {
                 int i = st.back(); st.pop_back();
-                if (d->nodes[i].kind == SANIC_NODE_REDUCE) has_reduce = true;
+                if (d->nodes[i].kind == SANIC_NODE_REDUCE || d->nodes[i].kind == SANIC_NODE_SCAN) has_reduce = true;
                 for (int q = 0; q < d->nodes[i].n_in; q++) st.push_back(d->nodes[i].in[q]);
             }
             if (!has_reduce) continue;

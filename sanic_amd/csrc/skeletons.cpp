@@ -628,7 +628,7 @@ static std::map<int, std::string> prefetch_epilogue(Renderer& R, Code& k, const 
         int ni = stack.back();
         stack.pop_back();
         const sanic_node& n = d->nodes[ni];
-        if (n.kind == SANIC_NODE_REDUCE || n.kind == SANIC_NODE_GATHER) return vars;
+        if (n.kind == SANIC_NODE_REDUCE || n.kind == SANIC_NODE_SCAN || n.kind == SANIC_NODE_GATHER) return vars;
         for (int j = 0; j < n.n_in; j++) stack.push_back(n.in[j]);
     }
     const std::string saved = R.fold_var;

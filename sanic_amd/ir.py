@@ -42,7 +42,7 @@ M_ADD, M_MUL, M_MAX, M_MIN, M_LSE = range(5)
 MONOID_IDENTITY = {M_ADD: 0.0, M_MUL: 1.0, M_MAX: -math.inf, M_MIN: math.inf, M_LSE: -math.inf}
 
 # node kinds
-INPUT, CONST, IOTA, COORDINATE, MAP, REDUCE, GATHER, VIEW, REINDEX, FOLD = range(10)
+INPUT, CONST, IOTA, COORDINATE, MAP, REDUCE, GATHER, VIEW, REINDEX, FOLD, SCAN = range(11)
 
 
 @dataclass(eq=False)
@@ -129,6 +129,13 @@ def reduce(src: Node, dim: int, monoid: int) -> Node:
     dim = dim % src.rank
     shape = src.shape[:dim] + src.shape[dim + 1:]
     return Node(REDUCE, shape, (src,), op=monoid, dim=dim)
+
+
+def scan(src: Node, dim: int, monoid: int) -> Node:
+    """Inclusive prefix fold along `dim` (ir.rs `scan`; interp.rs `eval_scan`): out[.., i, ..] =
+    monoid over src[.., 0..=i, ..]."""
+    dim = dim % src.rank
+    return Node(SCAN, src.shape, (src,), op=monoid, dim=dim)
 
 
 def gather(src: Node, index: Node, dim: int) -> Node:

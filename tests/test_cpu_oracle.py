@@ -382,3 +382,33 @@ def test_flash_prefill_graph_equals_fused_attention(window):
     np.testing.assert_allclose(got["Qr"], qr, rtol=0, atol=0)
     want = oracle.attention(qr, kr, vals["V"], 1 / np.sqrt(HD), mask=2 if window else 1, window=window)
     np.testing.assert_allclose(got["O"], rb(want), rtol=2 ** -7, atol=1e-6)
+
+
+def _scan_program(shape, dim, monoid):
+    p = Program()
+    x = p.input("X", shape, ir.F32)
+    p.pointwise("Y", ir.scan(x, dim, monoid), ir.F32)
+    return p
+
+
+def test_scan_known_answer():
+    """Add-scan of [2, -1, 3, 0.5, 4] (tests/laws.rs:715-730, the reference's fallback stage)."""
+    p = _scan_program((5,), 0, ir.M_ADD)
+    vals = {"X": np.array([2.0, -1.0, 3.0, 0.5, 4.0])}
+    np.testing.assert_array_equal(oracle.eval_node(p, ir.scan(p.node("X"), 0, ir.M_ADD), vals),
+                                  [2.0, 1.0, 4.0, 4.5, 8.5])
+    np.testing.assert_array_equal(oracle.run_program(p, vals)["Y"], [2.0, 1.0, 4.0, 4.5, 8.5])
+
+
+@pytest.mark.parametrize("dim", [0, 1])
+def test_scan_matches_numpy_cumulative_ops(dim):
+    """Every monoid along either axis against numpy's accumulate (inclusive prefix)."""
+    x = oracle.lcg(77, 6 * 7).reshape(6, 7) * 2.0
+    p = Program()
+    p.input("X", (6, 7), ir.F32)
+    want = {ir.M_ADD: np.add.accumulate(x, axis=dim), ir.M_MUL: np.multiply.accumulate(x, axis=dim),
+            ir.M_MAX: np.maximum.accumulate(x, axis=dim), ir.M_MIN: np.minimum.accumulate(x, axis=dim),
+            ir.M_LSE: np.logaddexp.accumulate(x, axis=dim)}
+    for m, w in want.items():
+        got = oracle.eval_node(p, ir.scan(p.node("X"), dim, m), {"X": x})
+        np.testing.assert_allclose(got, w, rtol=1e-12, atol=1e-12)

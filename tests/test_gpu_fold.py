@@ -84,3 +84,31 @@ def test_capture_feedback_converts_output_into_input(dev):
         rp.step()
     np.testing.assert_array_equal(xb.read(ir.F32, 8), np.arange(8) + 3.0)
     np.testing.assert_array_equal(rp.buffer("t").read(ir.U32, 8), np.arange(8) + 3)
+
+
+def test_prefix_scan_fallback_stage_known_answer(dev):
+    """The reference's scan known answer through a pointwise (fallback) stage on the GPU
+    (tests/laws.rs:715-730): exact."""
+    p = Program()
+    x = p.input("X", (5,), ir.F32)
+    p.pointwise("Y", ir.scan(x, 0, ir.M_ADD), ir.F32)
+    got, exe = run_on_gpu(dev, p, {"X": np.array([2.0, -1.0, 3.0, 0.5, 4.0])})
+    print(exe.stage_kernel(0))
+    np.testing.assert_array_equal(got["Y"], [2.0, 1.0, 4.0, 4.5, 8.5])
+
+
+@pytest.mark.parametrize("monoid", [ir.M_ADD, ir.M_MAX, ir.M_MIN, ir.M_LSE])
+@pytest.mark.parametrize("dim", [0, 1])
+def test_prefix_scan_matches_oracle(dev, monoid, dim):
+    """[24, 300] scans along either axis against the f64 interpreter: f32 ≤ 1e-4 with the
+    reference's metric; Max/Min exact."""
+    p = Program()
+    x = p.input("X", (24, 300), ir.F32)
+    p.pointwise("Y", ir.scan(x, dim, monoid), ir.F32)
+    vals = {"X": oracle.lcg(91, 24 * 300).reshape(24, 300)}
+    got, _ = run_on_gpu(dev, p, vals)
+    want = oracle.run_program(p, vals)["Y"]
+    if monoid in (ir.M_MAX, ir.M_MIN):
+        np.testing.assert_array_equal(got["Y"], want)
+    else:
+        assert max_rel_err(got["Y"], want) < 1e-4
