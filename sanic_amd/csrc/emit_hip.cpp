@@ -982,13 +982,62 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
         body.line("if (t == 0) sanic_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;");
         body.line("__syncthreads();");
         body.line("if (!sanic_last) return;");
-        body.line("for (idx_t gid = t; gid < " + std::to_string(gvol) + "; gid += " + std::to_string(nth) + ") {");
-        body.indent++;
-        R.memo.emplace_back();
-        merge_point(R, body);
-        R.memo.pop_back();
-        body.indent--;
-        body.line("}");
+        // Few output points: L = split rounded up to a power of two lanes per point load one
+        // partial each (all loads in flight at once) and merge in log2(L) butterfly steps of the
+        // carrier's combine, the lower partial index always on the left — the same order as the
+        // serial walk, so a first-index tie rule (AtExtremum) is kept. Otherwise one thread per
+        // point walks its partials.
+        int LPP = 1;
+        while (LPP < split) LPP <<= 1;
+        const bool butterfly = LPP <= 64 && gvol <= (int64_t)(nth / LPP) * 4 && !getenv("SANIC_FOLD_SERIAL_MERGE");
+        if (butterfly) {
+            const int PPP = nth / LPP;                 // points per pass
+            body.line("for (idx_t base = 0; base < " + std::to_string(gvol) + "; base += " + std::to_string(PPP) + ") {");
+            body.indent++;
+            body.line("const idx_t gid = base + t / " + std::to_string(LPP) + ";");
+            body.line("const int p = t % " + std::to_string(LPP) + ";");
+            body.line("const bool live = gid < " + std::to_string(gvol) + " && p < " + std::to_string(split) + ";");
+            body.line("const float* pp = a.scratch + ((gid < " + std::to_string(gvol) + " ? gid : 0) * " + std::to_string(split) + " + (p < " +
+                      std::to_string(split) + " ? p : 0)) * " + std::to_string(c.slots) + ";");
+            for (int k = 0; k < c.slots; k++)
+                body.line("float acc" + std::to_string(k) + " = live ? sanic_ld(pp + " + std::to_string(k) + ") : " + flit(c.identity[k]) + ";");
+            body.line("#pragma unroll");
+            body.line("for (int off = 1; off < " + std::to_string(LPP) + "; off <<= 1) {");
+            body.indent++;
+            body.line("const bool up = (p & off) != 0;");
+            for (int k = 0; k < c.slots; k++) {
+                std::string ks = std::to_string(k);
+                body.line("const float o" + ks + " = __shfl_xor(acc" + ks + ", off, 64);");
+                body.line("const float lo" + ks + " = up ? o" + ks + " : acc" + ks + ", hi" + ks + " = up ? acc" + ks + " : o" + ks + ";");
+            }
+            R.memo.emplace_back();
+            for (int k = 0; k < c.slots; k++) {
+                std::string v = R.expr(body, c.combine[k], "", "lo", "hi", "");
+                body.line("const float nx" + std::to_string(k) + " = " + v + ";");
+            }
+            R.memo.pop_back();
+            for (int k = 0; k < c.slots; k++) body.line("acc" + std::to_string(k) + " = nx" + std::to_string(k) + ";");
+            body.indent--;
+            body.line("}");
+            body.line("if (p == 0 && gid < " + std::to_string(gvol) + ") {");
+            body.indent++;
+            R.memo.emplace_back();
+            decode_grid(body, st, "gid");
+            emit_finish(R, body, st, "gid");
+            R.memo.pop_back();
+            body.indent--;
+            body.line("}");
+            body.indent--;
+            body.line("}");
+        } else {
+            body.line("for (idx_t gid = t; gid < " + std::to_string(gvol) + "; gid += " + std::to_string(nth) + ") {");
+            body.indent++;
+            R.memo.emplace_back();
+            merge_point(R, body);
+            R.memo.pop_back();
+            body.indent--;
+            body.line("}");
+        }
         for (int ts : tails) {
             body.line("__syncthreads();");
             emit_pointwise_loop(R, body, d, ts, "(idx_t)t", nth);

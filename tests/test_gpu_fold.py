@@ -112,3 +112,32 @@ def test_prefix_scan_matches_oracle(dev, monoid, dim):
         np.testing.assert_array_equal(got["Y"], want)
     else:
         assert max_rel_err(got["Y"], want) < 1e-4
+
+
+@pytest.mark.parametrize("split", [7, 37, 64])
+def test_split_merge_butterfly_keeps_first_index(dev, split):
+    """The last workgroup's butterfly merge (one lane per partial, identity-padded to a power
+    of two) keeps the serial walk's order: of three equal maxima in different partials the
+    first index wins, for splits that are and are not powers of two."""
+    n = 50_000
+    p = Program()
+    x = p.input("X", (n,))
+    p.fused("I", (1,), n, [(x, (STREAM,)), (ir.iota(n), (STREAM,))], C.first_argmax(), ir.U32,
+            sched=Sched(lane_stream=True, waves=4, chunk=4, split=split))
+    vals = oracle.lcg(7 + split, n)
+    for i in (n - 5, 31_000, 12_345):
+        vals[i] = 7.0
+    got, exe = run_on_gpu(dev, p, {"X": vals})
+    assert exe.stage_kernel(0).startswith("fold:split+merge")
+    assert int(got["I"][0]) == 12_345
+
+
+def test_split_merge_butterfly_small_grid_attention(dev):
+    """Config A at 16×8 with a 7-way split: 128 output points merged by butterflies of 8 lanes
+    (ExpShifted combine with its −∞ guard), against the interpreter."""
+    prog = configs.direct_attention(S=16, D=8, sched=Sched(lane_stream=True, waves=4, split=7))
+    vals = {n: oracle.lcg(s, 16 * 8).reshape(16, 8) for n, s in (("Q", 21), ("K", 22), ("V", 23))}
+    got, exe = run_on_gpu(dev, prog, vals)
+    assert exe.stage_kernel(0).startswith("fold:split+merge")
+    want = oracle.run_program(prog, vals)["O"]
+    assert max_rel_err(got["O"], want) < 1e-4
