@@ -240,6 +240,60 @@ static void check_binding(sanic_hip_exe* exe, int i, sanic_hip_buffer* b) {
     if (b->dev != exe->dev) fail(SANIC_ERR_ARG, "binding lives on another device");
 }
 
+// ── SANIC_DEBUG (the reference's debug levels, lib.rs:25-46, compile.rs:1141-1300) ─────────
+// 1: the compiled schedule at prepare (one line per stage: output buffer, kernel kind, launch
+//    shape, logical bytes); 2: one line per replay call with its GPU time and the fraction of
+//    the HBM peak its logical bytes reach; 3: the frozen graph's launches once at capture;
+//    4: the first step of each replay call runs stage by stage between GPU events and prints
+//    each stage's time, share and bandwidth. Logical bytes = sizes of the buffers a launch
+//    binds (an upper bound on its traffic), as the reference counts them.
+
+static const double kHbmBytesPerS = 8.0e12;   // MI355X HBM3E peak
+
+static int debug_level() {
+    static int level = [] {
+        const char* e = getenv("SANIC_DEBUG");
+        return e ? atoi(e) : 0;
+    }();
+    return level;
+}
+
+static double launch_bytes(const std::vector<sanic_buffer_desc>& buffers, const Launch& l) {
+    double b = 0;
+    for (auto& a : l.args)
+        if (a.kind == Arg::BUF) b += (double)buffer_bytes(buffers[a.v]);
+    return b;
+}
+
+static double stage_bytes(const std::vector<sanic_buffer_desc>& buffers, const LoweredStage& s) {
+    double b = 0;
+    for (auto& l : s.launches) b += launch_bytes(buffers, l);
+    return b;
+}
+
+static void dump_schedule(const char* what, const sanic_program_desc* d, const Lowered& low) {
+    std::vector<sanic_buffer_desc> buffers(d->buffers, d->buffers + d->n_buffers);
+    double total = 0;
+    fprintf(stderr, "*** hip %s: %d stages\n", what, (int)low.stages.size());
+    for (size_t i = 0; i < low.stages.size(); i++) {
+        const LoweredStage& s = low.stages[i];
+        const double mb = stage_bytes(buffers, s) / 1e6;
+        total += mb;
+        std::string shape;
+        for (auto& l : s.launches)
+            shape += " grid=(" + std::to_string(l.grid.x) + "," + std::to_string(l.grid.y) + ") block=" + std::to_string(l.block.x);
+        fprintf(stderr, "***   %4zu b%-4d %-44s%s ~%.1fMB\n", i, d->stages[i].out_buffer, s.kernel_kind.c_str(),
+                shape.empty() ? " (in another launch)" : shape.c_str(), mb);
+    }
+    fprintf(stderr, "*** hip %s: ~%.1fMB logical\n", what, total);
+}
+
+static double program_bytes(const sanic_hip_exe* exe) {
+    double b = 0;
+    for (auto& s : exe->low.stages) b += stage_bytes(exe->buffers, s);
+    return b;
+}
+
 // ── C ABI ────────────────────────────────────────────────────────────────────────────────
 
 extern "C" {
@@ -280,7 +334,7 @@ int sanic_hip_specs(sanic_hip_device* dev, sanic_device_specs* out) {
         out->compute_units = dev->props.multiProcessorCount;
         out->wave_size = dev->props.warpSize;
         out->lds_bytes_per_cu = 160 * 1024;
-        out->hbm_bytes_per_s = 8.0e12;             // MI355X HBM3E
+        out->hbm_bytes_per_s = kHbmBytesPerS;
         out->bf16_mfma_flops = 2.5e15;             // dense bf16 MFMA
         out->f32_flops = 157.3e12;
         out->clock_hz = dev->props.clockRate * 1000.0;
@@ -361,6 +415,7 @@ int sanic_hip_prepare(sanic_hip_device* dev, const sanic_program_desc* desc, san
             exe->stage_out_role.push_back(desc->buffers[desc->stages[s].out_buffer].role);
         }
         compile_all(exe.get(), true);
+        if (debug_level() >= 1) dump_schedule("schedule", desc, exe->low);
         *out = exe.release();
     });
 }
@@ -479,6 +534,16 @@ int sanic_hip_capture(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int
         }
         SANIC_HIP(hipStreamEndCapture(s, &rp->graph));
         SANIC_HIP(hipGraphInstantiate(&rp->graph_exec, rp->graph, nullptr, nullptr, 0));
+        if (debug_level() >= 3) {
+            int nl = 0;
+            for (auto& st : exe->low.stages) nl += (int)st.launches.size();
+            fprintf(stderr, "*** hip graph: %d launches + %zu feedback conversions, ~%.1fMB logical\n", nl,
+                    rp->feedback.size(), program_bytes(exe) / 1e6);
+            for (size_t i = 0; i < exe->low.stages.size(); i++)
+                for (auto& l : exe->low.stages[i].launches)
+                    fprintf(stderr, "***   %4zu %-32s grid=(%u,%u) block=%u lds=%u ~%.1fMB\n", i, l.kernel.c_str(), l.grid.x,
+                            l.grid.y, l.block.x, l.lds, launch_bytes(exe->buffers, l) / 1e6);
+        }
         SANIC_HIP(hipEventCreate(&rp->ev0));
         SANIC_HIP(hipEventCreate(&rp->ev1));
         *out = rp.release();
@@ -501,13 +566,55 @@ int sanic_hip_step_many(sanic_hip_replay* rp, int n, double* gpu_seconds) {
         if (!rp || n < 1) fail(SANIC_ERR_ARG, "bad replay");
         hipStream_t s = rp->exe->dev->stream;
         SANIC_HIP(hipSetDevice(rp->exe->dev->ordinal));
+        const double peak = kHbmBytesPerS;
+        int first = 0;
+        double first_s = 0;
+        if (debug_level() >= 4) {
+            // the first step stage by stage between GPU events (the step itself, not a re-run)
+            const auto& st = rp->exe->low.stages;
+            std::vector<hipEvent_t> ev(st.size() + 1);
+            for (auto& e : ev) SANIC_HIP(hipEventCreate(&e));
+            enqueue(rp->exe, rp->bound, rp->scratch->ptr(), ev.data());
+            SANIC_HIP(hipEventSynchronize(ev[st.size()]));
+            float tot = 0;
+            SANIC_HIP(hipEventElapsedTime(&tot, ev[0], ev[st.size()]));
+            for (size_t i = 0; i < st.size(); i++) {
+                if (st[i].launches.empty()) continue;
+                float ms = 0;
+                hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+                const double bytes = stage_bytes(rp->exe->buffers, st[i]);
+                fprintf(stderr, "*** hip  %4zu b%-4d %9.1fus %5.1f%%  ~%8.1fMB bw %3.0f%%  %s\n", i, rp->exe->stage_out[i], ms * 1e3,
+                        100.0 * ms / std::max(tot, 1e-9f), bytes / 1e6, 100.0 * bytes / std::max(ms * 1e-3, 1e-12) / peak,
+                        st[i].kernel_kind.c_str());
+            }
+            fprintf(stderr, "*** hip  stage-by-stage step %.1fus (between events: includes each stage's launch)\n", tot * 1e3);
+            for (auto& e : ev) hipEventDestroy(e);
+            first = 1;
+            first_s = tot * 1e-3;
+            // feedback conversions of that step
+            for (auto& fb : rp->feedback) {
+                const auto& ob = rp->exe->buffers[fb.first];
+                const auto& ib = rp->exe->buffers[fb.second];
+                int64_t cnt = 1;
+                for (int k = 0; k < ob.rank; k++) cnt *= ob.shape[k];
+                hipLaunchKernelGGL(sanic_convert, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, s,
+                                   (const void*)rp->bound[fb.first]->ptr(), ob.dtype, (void*)rp->bound[fb.second]->ptr(), ib.dtype, cnt);
+            }
+            SANIC_HIP(hipStreamSynchronize(s));
+        }
         SANIC_HIP(hipEventRecord(rp->ev0, s));
-        for (int i = 0; i < n; i++) SANIC_HIP(hipGraphLaunch(rp->graph_exec, s));
+        for (int i = first; i < n; i++) SANIC_HIP(hipGraphLaunch(rp->graph_exec, s));
         SANIC_HIP(hipEventRecord(rp->ev1, s));
         SANIC_HIP(hipEventSynchronize(rp->ev1));
         float ms = 0;
         SANIC_HIP(hipEventElapsedTime(&ms, rp->ev0, rp->ev1));
-        if (gpu_seconds) *gpu_seconds = ms * 1e-3;
+        const double secs = ms * 1e-3 + first_s;
+        if (gpu_seconds) *gpu_seconds = secs;
+        if (debug_level() >= 2) {
+            const double per = secs / n, bytes = program_bytes(rp->exe);
+            fprintf(stderr, "*** hip batched %zu stages x%d %8.3fms GPU per step  ~%.0fMB bw %3.0f%%\n", rp->exe->low.stages.size(), n,
+                    per * 1e3, bytes / 1e6, 100.0 * bytes / std::max(per, 1e-12) / peak);
+        }
     });
 }
 
@@ -569,6 +676,7 @@ int sanic_hip_precompile(const sanic_program_desc* desc) {
     return guarded([&] {
         sanic_hip_exe exe;
         exe.low = lower_program(desc);
+        if (debug_level() >= 1) dump_schedule("schedule", desc, exe.low);
         compile_all(&exe, false);
     });
 }
