@@ -1264,6 +1264,131 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const sanic_stage& st = d->stages[si];
     const sanic_carrier& c = st.carrier;
     const int64_t N = P.N, K = P.K;
+    // Strip form: a workgroup owns 32 columns over the whole K, so no K slices meet across
+    // workgroups. The activation factors of every k (and the row slots) are computed once into
+    // LDS; lane l reads 8 columns (16 bytes) of row (l / 4) of each 16-row step, the 4 waves take
+    // a quarter of K each; lanes of one column group meet by shuffles, waves in LDS. Strips are
+    // dealt XCD-aware: workgroups b and b + 8 (one XCD) own adjacent strips, so the two halves of
+    // a 128-byte line are read through the same L2.
+    int SW = 32;                                  // strip width (columns); 64 measured slower
+    if (const char* e = getenv("SANIC_GEMVT_SW")) SW = atoi(e) <= 32 ? 32 : 64;
+    const int NT = SW == 64 ? 512 : 256;          // 32 row loads per lane either way
+    const int LPR = SW / 8, RPS = 64 / LPR, NWV = NT / 64;   // lanes per row, rows per step, waves
+    if (N % (SW * 8) == 0 && K % (RPS * NWV) == 0 && K <= 8192 && !getenv("SANIC_GEMVT_SLICES")) {
+        const int SC = (int)P.cslots.size(), SR = (int)P.rslots.size();
+        const int64_t NS = N / SW, KQ = K / NWV, IT = KQ / RPS;   // strips, rows per wave, row steps
+        Renderer R(d);
+        Code k;
+        k.indent = 1;
+        k.line("__shared__ float fl[" + std::to_string(std::max(SC, 1)) + "][" + std::to_string(K) + "];");
+        k.line("__shared__ __attribute__((aligned(16))) float red[" + std::to_string(NWV) + "][" + std::to_string(SC * SW) + "];");
+        if (SR) k.line("__shared__ float rred[" + std::to_string(NWV) + "][" + std::to_string(SR) + "];");
+        k.line("const int t = threadIdx.x, lane = t & 63, wv = t >> 6;");
+        k.line("const idx_t strip = (blockIdx.x % 8) * " + std::to_string(NS / 8) + " + blockIdx.x / 8;");
+        k.line("const idx_t n0 = strip * " + std::to_string(SW) + " + (lane & " + std::to_string(LPR - 1) + ") * 8;");
+        // weight loads first (every row step of this lane), then the LDS prologue
+        std::vector<std::vector<std::string>> wv_(IT);
+        Code wdc;
+        wdc.indent = k.indent;
+        for (int64_t i = 0; i < IT; i++) {
+            VecW vw{d};
+            vw.nn = "((idx_t)wv * " + std::to_string(KQ) + " + " + std::to_string(i * RPS) + " + (lane / " + std::to_string(LPR) + "))";
+            vw.k0 = "n0";
+            vw.ptr = "wb";
+            vw.psfx = "";
+            vw.sfx = "_" + std::to_string(i);
+            Code l1;
+            l1.indent = k.indent;
+            wv_[i] = vw.render(l1, wdc, st.leaf[P.w], weight_coords(d, st, P.w, P.ndim, true), {K, N});
+            if (!vw.ok) return false;
+            if (i == 0)
+                for (size_t b = 0; b < vw.bufs.size(); b++)
+                    k.line("const " + std::string(ctype_of(vw.dtypes[b])) + "* __restrict__ wb" + std::to_string(b) + " = " + R.param(vw.bufs[b]) + ";");
+            k.s << l1.str();
+        }
+        // activation factors of every k into LDS; this workgroup's row slots
+        for (int r = 0; r < SR; r++) k.line("float rpart" + std::to_string(r) + " = 0.0f;");
+        k.line("for (int kr = t; kr < " + std::to_string(K) + "; kr += " + std::to_string(NT) + ") {");
+        k.indent++;
+        R.memo.emplace_back();
+        for (int l = 0; l < st.n_leaves; l++) {
+            if (l == P.w) continue;
+            const sanic_node& ln = d->nodes[st.leaf[l]];
+            std::vector<std::string> lc(ln.rank);
+            for (int j = 0; j < ln.rank; j++) lc[j] = st.bind[l][j] == SANIC_BIND_STREAM ? "kr" : "0";
+            k.line("const float x" + std::to_string(l) + " = " + R.value(k, st.leaf[l], lc) + ";");
+        }
+        for (int cs = 0; cs < SC; cs++)
+            k.line("fl[" + std::to_string(cs) + "][kr] = " + expr_without(R, k, c.into[P.cslots[cs]], P.w, "x") + ";");
+        for (int r = 0; r < SR; r++) k.line("rpart" + std::to_string(r) + " += " + R.expr(k, c.into[P.rslots[r]], "x", "", "", "") + ";");
+        R.memo.pop_back();
+        k.indent--;
+        k.line("}");
+        for (int r = 0; r < SR; r++) {
+            std::string rs = std::to_string(r);
+            k.line("for (int off = 32; off > 0; off >>= 1) rpart" + rs + " += __shfl_xor(rpart" + rs + ", off, 64);");
+            k.line("if (lane == 0) rred[wv][" + rs + "] = rpart" + rs + ";");
+        }
+        k.line("__syncthreads();");
+        k.s << wdc.str();
+        for (int cs = 0; cs < SC; cs++)
+            for (int j = 0; j < 8; j++) k.line("float acc" + std::to_string(cs) + "_" + std::to_string(j) + " = 0.0f;");
+        for (int64_t i = 0; i < IT; i++) {
+            const std::string kr = "((int)wv * " + std::to_string(KQ) + " + " + std::to_string(i * RPS) + " + (lane / " + std::to_string(LPR) + "))";
+            for (int cs = 0; cs < SC; cs++) {
+                const std::string f = "f" + std::to_string(cs) + "_" + std::to_string(i);
+                k.line("const float " + f + " = fl[" + std::to_string(cs) + "][" + kr + "];");
+                for (int j = 0; j < 8; j++) {
+                    std::string a = "acc" + std::to_string(cs) + "_" + std::to_string(j);
+                    k.line(a + " = fmaf(" + f + ", " + wv_[i][j] + ", " + a + ");");
+                }
+            }
+        }
+        // the 16 row lanes of each column group, then the 4 waves
+        for (int cs = 0; cs < SC; cs++)
+            for (int j = 0; j < 8; j++) {
+                std::string a = "acc" + std::to_string(cs) + "_" + std::to_string(j);
+                k.line("for (int off = " + std::to_string(LPR) + "; off < 64; off <<= 1) " + a + " += __shfl_xor(" + a + ", off, 64);");
+            }
+        k.line("if (lane < " + std::to_string(LPR) + ") {");
+        for (int cs = 0; cs < SC; cs++) {
+            std::string css = std::to_string(cs), base = css + " * " + std::to_string(SW);
+            k.line("  *(sanic_f32x4*)(&red[wv][" + base + " + lane * 8]) = (sanic_f32x4){acc" + css + "_0, acc" + css + "_1, acc" + css + "_2, acc" + css + "_3};");
+            k.line("  *(sanic_f32x4*)(&red[wv][" + base + " + lane * 8 + 4]) = (sanic_f32x4){acc" + css + "_4, acc" + css + "_5, acc" + css + "_6, acc" + css + "_7};");
+        }
+        k.line("}");
+        k.line("__syncthreads();");
+        k.line("if (t < " + std::to_string(SW) + ") {");
+        k.indent++;
+        k.line("const idx_t nn = strip * " + std::to_string(SW) + " + t;");
+        std::string arr = "const float accq[" + std::to_string(std::max(SC, 1)) + "] = {";
+        for (int cs = 0; cs < SC; cs++) {
+            std::string i = std::to_string(cs) + " * " + std::to_string(SW) + " + t", sum = "red[0][" + i + "]";
+            for (int w = 1; w < NWV; w++) sum = "(" + sum + " + red[" + std::to_string(w) + "][" + i + "])";
+            arr += std::string(cs ? ", " : "") + sum;
+        }
+        if (SC == 0) arr += "0.0f";
+        k.line(arr + "};");
+        for (int r = 0; r < SR; r++) {
+            std::string rs = std::to_string(r);
+            std::string sum = "rred[0][" + rs + "]";
+            for (int w = 1; w < NWV; w++) sum = "(" + sum + " + rred[" + std::to_string(w) + "][" + rs + "])";
+            k.line("const float racc" + rs + " = " + sum + ";");
+        }
+        R.memo.emplace_back();
+        gemv_finish(R, k, d, P, false);
+        R.memo.pop_back();
+        k.indent--;
+        k.line("}");
+        const std::string kname = "sanic_gemvt_" + std::to_string(N) + "x" + std::to_string(K);
+        std::ostringstream src;
+        src << kPrelude << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(" << NT << ") " << kname << "(Args a) {\n"
+            << R.entry() << k.str() << "}\n";
+        out.kernel_kind = "skeleton:gemv_kmajor[strips " + std::to_string(SW) + "]";
+        out.source = src.str();
+        out.launches.push_back({kname, "", dim3((unsigned)NS), dim3((unsigned)NT), 0, R.arg_list()});
+        return true;
+    }
     if (N % 512 || K % 64) return false;
     const int SC = (int)P.cslots.size(), SR = (int)P.rslots.size();
     const int64_t NCG = N / 512;
@@ -1402,7 +1527,7 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     std::ostringstream src;
     src << kPrelude << R.args_struct({"float* __restrict__ scratch"})
         << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
-    out.kernel_kind = "skeleton:gemv_kmajor[" + std::to_string(KS) + " slices]";
+    out.kernel_kind = "skeleton:gemv_kmajor[" + std::to_string(KS) + " slices]";   // the strip form's fallback
     out.source = src.str();
     std::vector<Arg> args = R.arg_list();
     args.push_back({Arg::SCRATCH, 0});
