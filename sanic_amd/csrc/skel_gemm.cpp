@@ -177,8 +177,18 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     const int MT = WM / 16, NT = WN / 16;
     const int SR = (int)P.rslots.size();
     int AS = 64 + 8;                          // LDS row strides (bf16)
-    const int BS = 64 + 8;
+    int BS = 64 + 8;
     if (const char* e = getenv("SANIC_GEMM_AS")) AS = std::max(64, atoi(e) / 8 * 8);
+    // k-contiguous tiles: unpadded 128-byte rows with the 16-byte chunk index XORed by
+    // (row mod 8) — a 72-element padded stride 2-way bank-conflicts the 16-row operand reads
+    // on gfx950
+    const bool kswz = !getenv("SANIC_GEMM_APAD") && !getenv("SANIC_GEMM_AS");
+    if (kswz) AS = BS = 64;
+    // element offset of (row, k) in a k-contiguous tile; k a multiple of 8
+    auto koff = [&](const std::string& row, const std::string& k8, int stride) {
+        if (kswz) return "(" + row + ") * 64 + (((" + k8 + ") / 8) ^ ((" + row + ") & 7)) * 8";
+        return "(" + row + ") * " + std::to_string(stride) + " + " + k8;
+    };
     // An operand that is not a bf16 input as stored (x·g, dequantized weights) goes to the MFMA
     // as hi + lo bf16 pair (hi = rn(v), lo = rn(v − hi): 16 significant bits, exact for the
     // product of two bf16 values), so products match an f32 evaluation; one extra MFMA each.
@@ -420,7 +430,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         c2.line("const int ar = tid / " + std::to_string(TPR) + ";");
         for (int r = 0; r < RUNS_A && pre; r++) {
             const std::string rs = std::to_string(r);
-            const std::string aoff = "ar * " + std::to_string(AS) + " + (tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8);
+            const std::string aoff = koff("ar", "(tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8), AS);
             c2.line("*(sanic_u32x4*)(&a_lds[" + buf + "][" + aoff + "]) = pah" + rs + sfx + ";");
             c2.line("*(sanic_u32x4*)(&a_lo[" + buf + "][" + aoff + "]) = pal" + rs + sfx + ";");
         }
@@ -442,7 +452,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
                     c2.line("racc" + std::to_string(sidx) + " += " + rv + ";");
                 }
             }
-            const std::string aoff = "ar * " + std::to_string(AS) + " + (tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8);
+            const std::string aoff = koff("ar", "(tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8), AS);
             if (splitA) {
                 const std::string h = R.fresh("ah"), l = R.fresh("al");
                 c2.line("unsigned " + h + "[4], " + l + "[4];");
@@ -471,8 +481,9 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
                 row = "(tid % " + std::to_string(BN) + ")";
                 col = "(((tid / " + std::to_string(BN) + ") + " + std::to_string(r * (256 / BN)) + ") * 8)";
             }
-            c2.line("*(sanic_u32x4*)(&b_lds[" + buf + "][" + row + " * " + std::to_string(stride) + " + " + col + "]) = rb" + rs + sfx + ";");
-            if (splitB) c2.line("*(sanic_u32x4*)(&b_lo[" + buf + "][" + row + " * " + std::to_string(stride) + " + " + col + "]) = rl" + rs + sfx + ";");
+            const std::string boff = bkn ? row + " * " + std::to_string(stride) + " + " + col : koff(row, col, stride);
+            c2.line("*(sanic_u32x4*)(&b_lds[" + buf + "][" + boff + "]) = rb" + rs + sfx + ";");
+            if (splitB) c2.line("*(sanic_u32x4*)(&b_lo[" + buf + "][" + boff + "]) = rl" + rs + sfx + ";");
         }
         c2.indent--;
         c2.line("}");
@@ -481,8 +492,8 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         c2.line("#pragma unroll");
         c2.line("for (int ks = 0; ks < 2; ++ks) {");
         const std::string MTs = std::to_string(MT), NTs = std::to_string(NT);
-        const std::string aidx = "[(wm + i * 16 + l16) * " + std::to_string(AS) + " + ks * 32 + lq * 8]";
-        const std::string bidx = "[(wn + j * 16 + l16) * " + std::to_string(BS) + " + ks * 32 + lq * 8]";
+        const std::string aidx = "[" + koff("wm + i * 16 + l16", "ks * 32 + lq * 8", AS) + "]";
+        const std::string bidx = "[" + koff("wn + j * 16 + l16", "ks * 32 + lq * 8", BS) + "]";
         c2.line("  bf16x8 af[" + MTs + "], bf[" + NTs + "];");
         if (splitA) c2.line("  bf16x8 afl[" + MTs + "];");
         if (splitB) c2.line("  bf16x8 bfl[" + NTs + "];");
