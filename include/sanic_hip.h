@@ -53,18 +53,24 @@ enum {
  * Storage dtypes (/root/reference/src/scalar.rs:180-326 `Dtype`). U4 is the unsigned nibble
  * form used by asymmetric group quantisation (value = u); I4 is the reference's signed nibble
  * (value = u - 8, emit_metal.rs:179-181). Both pack two values per byte, low nibble = even index.
+ * Q8 is the reference's affine-quantized byte `Dtype::Q8 { scale }` (scalar.rs:190-198): one
+ * signed byte q per element, value q·scale, the scale carried by the buffer
+ * (`sanic_buffer_desc.scale`); stores round v/scale to the nearest integer in f32 and clamp it
+ * to ±127 (emit_metal.rs:182-185, 226-229), so ±∞ land on ±127·scale.
  * ------------------------------------------------------------------------------------------- */
 enum {
     SANIC_F64 = 0, SANIC_F32 = 1, SANIC_F16 = 2, SANIC_BF16 = 3, SANIC_U32 = 4,
-    SANIC_I8 = 5, SANIC_I4 = 6, SANIC_U4 = 7
+    SANIC_I8 = 5, SANIC_I4 = 6, SANIC_U4 = 7, SANIC_Q8 = 8
 };
 
-/* MapOp (/root/reference/src/scalar.rs:45-69). ROUND_BF16/ROUND_F32 are `RoundTo(dtype)`. */
+/* MapOp (/root/reference/src/scalar.rs:45-69). ROUND_BF16/ROUND_F32 are `RoundTo(dtype)`;
+ * ROUND_Q8 is `RoundTo(Q8 { scale })` with the scale in the MAP node's `value`
+ * (emit_metal.rs:100-103: the value a Q8 store+load would give); nodes only, not carrier Exprs. */
 enum {
     SANIC_OP_ADD = 0, SANIC_OP_SUB, SANIC_OP_MUL, SANIC_OP_DIV, SANIC_OP_MAX, SANIC_OP_MIN,
     SANIC_OP_LT, SANIC_OP_NEG, SANIC_OP_RECIP, SANIC_OP_EXP, SANIC_OP_LOG, SANIC_OP_SQRT,
     SANIC_OP_TANH, SANIC_OP_SIN, SANIC_OP_COS, SANIC_OP_WHERE, SANIC_OP_ROUND_BF16,
-    SANIC_OP_ROUND_F32
+    SANIC_OP_ROUND_F32, SANIC_OP_ROUND_Q8
 };
 
 /* Monoid (/root/reference/src/scalar.rs:18-41). */
@@ -113,7 +119,7 @@ typedef struct sanic_node {
     int32_t group[SANIC_MAX_RANK]; /* VIEW                                            */
     int32_t padded;      /* REINDEX                                                   */
     int32_t map_offset;  /* REINDEX: offset into the reindex table                   */
-    double value;        /* CONST                                                     */
+    double value;        /* CONST; MAP ROUND_Q8: the scale                            */
 } sanic_node;
 
 /* ---------------------------------------------------------------------------------------------
@@ -208,6 +214,7 @@ typedef struct sanic_buffer_desc {
     int32_t role;
     int32_t dtype;
     int32_t rank;
+    float scale;                 /* Q8: the grid step (value = q·scale); ignored otherwise */
     int64_t shape[SANIC_MAX_RANK];
 } sanic_buffer_desc;
 

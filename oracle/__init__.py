@@ -36,6 +36,8 @@ def lib():
         L.oracle_round_bf16.argtypes = [ctypes.c_double]
         L.oracle_round_to.restype = ctypes.c_double
         L.oracle_round_to.argtypes = [ctypes.c_int, ctypes.c_double]
+        L.oracle_round_q8.restype = ctypes.c_double
+        L.oracle_round_q8.argtypes = [ctypes.c_double, ctypes.c_double]
         L.oracle_eval.argtypes = [VP, ctypes.c_int, VP, VP]
         L.oracle_fold_stage.argtypes = [VP, ctypes.c_int, VP, ctypes.c_int, VP, VP]
         L.oracle_run_stage.argtypes = [VP, ctypes.c_int, VP, ctypes.c_int]
@@ -82,6 +84,11 @@ def f64(a) -> np.ndarray:
 
 def round_bf16(v: float) -> float:
     return lib().oracle_round_bf16(float(v))
+
+
+def round_q8(scale: float, v: float) -> float:
+    """round_to(Q8 { scale }, v) (scalar.rs:143-147)."""
+    return lib().oracle_round_q8(float(scale), float(v))
 
 
 def lcg(seed: int, n: int) -> np.ndarray:
@@ -158,6 +165,7 @@ def eval_node(prog, node, values) -> np.ndarray:
     bufs = np.zeros(len(prog.buffers), dtype=abi.BUFFER_DT)
     for i, b in enumerate(prog.buffers):
         bufs[i]["role"], bufs[i]["dtype"], bufs[i]["rank"] = b.role, b.dtype, len(b.shape)
+        bufs[i]["scale"] = ir.dtype_scale(b.dtype)
         bufs[i]["shape"] = list(b.shape) + [0] * (abi.MAX_RANK - len(b.shape))
     desc = abi.ProgramDesc(len(nodes), nodes.ctypes.data, 0, None, len(nt.reindex),
                            reindex.ctypes.data, len(bufs), bufs.ctypes.data, 0, None)

@@ -45,6 +45,15 @@ double oracle_round_bf16(double v) {
     return (double)f;
 }
 
+/* scalar.rs:143-147: the Q8 grid {q·scale : −127 ≤ q ≤ 127}, q = round(v/scale) with ties
+   away from zero (f64::round), clamped; grid points are fixed points */
+double oracle_round_q8(double scale, double v) {
+    double q = round(v / scale);
+    if (q < -127.0) q = -127.0;
+    if (q > 127.0) q = 127.0;
+    return q * scale;
+}
+
 double oracle_round_to(int dtype, double v) {
     switch (dtype) {
     case SANIC_F64: return v;
@@ -201,7 +210,7 @@ static const double* eval_node(ctx_t* cx, int idx) {
                 for (int j = 0; j < m->rank; j++) s[j] = m->shape[j] == 1 ? 0 : c[lead + j];
                 args[k] = ins[k][flatten_at(s, m->shape, m->rank)];
             }
-            out[i] = oracle_apply_map(n->op, args);
+            out[i] = n->op == SANIC_OP_ROUND_Q8 ? oracle_round_q8(n->value, args[0]) : oracle_apply_map(n->op, args);
         }
         break;
     }
@@ -390,6 +399,12 @@ int oracle_fold_stage(const sanic_program_desc* d, int stage, double* const* buf
 }
 
 /* Execute one stage into its output buffer, narrowing through the stored dtype. */
+/* the stage's narrowing store: round_to of its storage dtype, Q8 with the buffer's scale */
+static double store_round(const sanic_program_desc* d, const sanic_stage* st, double v) {
+    if (st->out_dtype == SANIC_Q8) return oracle_round_q8((double)d->buffers[st->out_buffer].scale, v);
+    return oracle_round_to(st->out_dtype, v);
+}
+
 int oracle_run_stage(const sanic_program_desc* d, int stage, double* const* buffers, int blocks) {
     const sanic_stage* st = &d->stages[stage];
     int64_t gvol = 1;
@@ -407,7 +422,7 @@ int oracle_run_stage(const sanic_program_desc* d, int stage, double* const* buff
             memcpy(val, e, sizeof(double) * (size_t)gvol);
             ctx_free(&cx);
         }
-        for (int64_t i = 0; i < gvol; i++) out[i] = oracle_round_to(st->out_dtype, val[i]);
+        for (int64_t i = 0; i < gvol; i++) out[i] = store_round(d, st, val[i]);
     } else {
         ctx_t cx;
         ctx_init(&cx, d, buffers, NULL);
@@ -426,7 +441,7 @@ int oracle_run_stage(const sanic_program_desc* d, int stage, double* const* buff
             }
             int lead = st->rank - vn->rank;
             for (int j = 0; j < vn->rank; j++) s[j] = vn->shape[j] == 1 ? 0 : g[lead + j];
-            out[i] = oracle_round_to(st->out_dtype, v[flatten_at(s, vn->shape, vn->rank)]);
+            out[i] = store_round(d, st, v[flatten_at(s, vn->shape, vn->rank)]);
         }
         ctx_free(&cx);
     }

@@ -20,6 +20,7 @@ extern "C" {
 /* scalar.rs:120-152 */
 double oracle_round_bf16(double v);
 double oracle_round_to(int dtype, double v);
+double oracle_round_q8(double scale, double v);
 double oracle_apply_map(int op, const double* a);
 double oracle_monoid_identity(int m);
 double oracle_monoid_combine(int m, double a, double b);

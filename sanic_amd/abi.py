@@ -46,7 +46,7 @@ STAGE_DT = np.dtype([
     ("where", "<i4"),
 ], align=True)
 
-BUFFER_DT = np.dtype([("role", "<i4"), ("dtype", "<i4"), ("rank", "<i4"),
+BUFFER_DT = np.dtype([("role", "<i4"), ("dtype", "<i4"), ("rank", "<i4"), ("scale", "<f4"),
                       ("shape", "<i8", MAX_RANK)], align=True)
 
 

@@ -60,6 +60,10 @@ def encode(values: np.ndarray, dtype: int) -> bytes:
         return np.ascontiguousarray(v, dtype=np.uint32).tobytes()
     if dtype == ir.I8:
         return np.ascontiguousarray(v, dtype=np.int8).tobytes()
+    if dtype == ir.Q8:
+        # the device's store rule: v/scale in f32, half-to-even, clamped to ±127
+        q = np.rint(np.asarray(v, np.float32) / np.float32(ir.dtype_scale(dtype)))
+        return np.clip(np.nan_to_num(q, nan=-127.0), -127, 127).astype(np.int8).tobytes()
     if dtype == ir.I4:
         return pack_nibbles(np.asarray(v, dtype=np.int64) + 8).tobytes()
     if dtype == ir.U4:
@@ -77,6 +81,8 @@ def decode(raw: bytes, dtype: int, n: int) -> np.ndarray:
         return np.frombuffer(raw, np.float16, n).astype(np.float64)
     if dtype == ir.U32:
         return np.frombuffer(raw, np.uint32, n).astype(np.float64)
+    if dtype == ir.Q8:   # q·scale in f32, as the device's load computes it
+        return (np.frombuffer(raw, np.int8, n).astype(np.float32) * np.float32(ir.dtype_scale(dtype))).astype(np.float64)
     if dtype == ir.I8:
         return np.frombuffer(raw, np.int8, n).astype(np.float64)
     b = np.frombuffer(raw, np.uint8)

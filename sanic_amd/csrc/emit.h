@@ -56,7 +56,8 @@ const char* ctype_of(int dt);
 std::string map_expr(int op, const std::string& a, const std::string& b, const std::string& c);
 std::string monoid_combine(int m, const std::string& a, const std::string& b);
 double monoid_identity(int m);
-std::string store_stmt(const std::string& ptr, const std::string& idx, int dt, const std::string& v, bool coherent = false);
+std::string store_stmt(const std::string& ptr, const std::string& idx, int dt, const std::string& v, bool coherent = false,
+                       double scale = 0.0);
 void decode_grid(Code& code, const sanic_stage& st, const std::string& gid);
 std::vector<std::string> leaf_coords(const sanic_stage& st, const sanic_program_desc* d, int l,
                                      const std::string& s);

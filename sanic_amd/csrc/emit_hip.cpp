@@ -41,7 +41,7 @@ int64_t dtype_bytes(int dt, int64_t n) {
     case SANIC_F64: return 8 * n;
     case SANIC_F32: case SANIC_U32: return 4 * n;
     case SANIC_F16: case SANIC_BF16: return 2 * n;
-    case SANIC_I8: return n;
+    case SANIC_I8: case SANIC_Q8: return n;
     case SANIC_I4: case SANIC_U4: return (n + 1) / 2;
     }
     fail(SANIC_ERR_DTYPE, "unknown dtype " + std::to_string(dt));
@@ -74,7 +74,8 @@ static void check_node(const sanic_program_desc* d, int i) {
     case SANIC_NODE_FOLD: break;
     case SANIC_NODE_MAP: {
         int ar = (n.op == SANIC_OP_WHERE) ? 3 : (n.op <= SANIC_OP_LT ? 2 : 1);
-        if (n.op < 0 || n.op > SANIC_OP_ROUND_F32 || n.n_in != ar) bad("map arity");
+        if (n.op < 0 || n.op > SANIC_OP_ROUND_Q8 || n.n_in != ar) bad("map arity");
+        if (n.op == SANIC_OP_ROUND_Q8 && !(n.value > 0.0)) bad("Q8 rounding needs a positive scale");
         for (int k = 0; k < n.n_in; k++) {
             const sanic_node& c = child(k);
             if (c.rank > n.rank) bad("map input rank exceeds output rank");
@@ -179,6 +180,7 @@ void validate(const sanic_program_desc* d) {
     for (int b = 0; b < d->n_buffers; b++) {
         const sanic_buffer_desc& bd = d->buffers[b];
         if (bd.rank < 0 || bd.rank > SANIC_MAX_RANK) fail(SANIC_ERR_COMPILE, "buffer rank");
+        if (bd.dtype == SANIC_Q8 && !(bd.scale > 0.0f)) fail(SANIC_ERR_DTYPE, "Q8 buffer without a positive scale");
         if (bd.role < SANIC_BUF_INPUT || bd.role > SANIC_BUF_SCRATCH) fail(SANIC_ERR_COMPILE, "buffer role");
         dtype_bytes(bd.dtype, 1);
     }
@@ -264,6 +266,11 @@ __device__ __forceinline__ unsigned sanic_to_u32(float v) {
   if (!(v > 0.0f)) return 0u;
   return (unsigned)(v + 0.5f);
 }
+// Q8 store: v/s rounded half-to-even in f32, clamped to the signed grid ±127 (a NaN lands on
+// −127, as with a NaN-ignoring clamp)
+__device__ __forceinline__ signed char sanic_to_q8(float v, float s) {
+  return (signed char)__builtin_fminf(__builtin_fmaxf(__builtin_rintf(v / s), -127.0f), 127.0f);
+}
 __device__ __forceinline__ float sanic_w4(const unsigned char* p, idx_t i) {
   return (float)(int)((p[i >> 1] >> ((i & 1) << 2)) & 0xF) - 8.0f;
 }
@@ -298,7 +305,7 @@ const char* ctype_of(int dt) {
     case SANIC_F16: return "_Float16";
     case SANIC_BF16: return "unsigned short";
     case SANIC_U32: return "unsigned";
-    case SANIC_I8: return "signed char";
+    case SANIC_I8: case SANIC_Q8: return "signed char";
     case SANIC_I4: case SANIC_U4: return "unsigned char";
     }
     return "float";
@@ -403,6 +410,7 @@ std::string Renderer::load(int node, const std::vector<std::string>& c) {
         case SANIC_F32: return a;
         case SANIC_BF16: return "sanic_bf16(" + a + ")";
         case SANIC_F16: case SANIC_U32: case SANIC_I8: return "(float)" + a;
+        case SANIC_Q8: return "((float)" + a + " * " + flit(d->buffers[n.buffer].scale) + ")";
         }
     }
     switch (n.dtype) {
@@ -411,6 +419,8 @@ std::string Renderer::load(int node, const std::vector<std::string>& c) {
     case SANIC_BF16: return "sanic_bf16(" + p + "[" + lin + "])";
     case SANIC_U32: return "(float)" + p + "[" + lin + "]";
     case SANIC_I8: return "(float)" + p + "[" + lin + "]";
+    // dequantization is the load: the buffer's scale as a literal (emit_metal.rs:134-137)
+    case SANIC_Q8: return "((float)" + p + "[" + lin + "] * " + flit(d->buffers[n.buffer].scale) + ")";
     case SANIC_I4: return "sanic_w4(" + p + ", " + lin + ")";
     case SANIC_U4: return "sanic_u4(" + p + ", " + lin + ")";
     }
@@ -460,7 +470,10 @@ std::string Renderer::value(Code& code, int node, const std::vector<std::string>
             a[k] = value(code, n.in[k], cc);
         }
         out = fresh("m");
-        code.line("const float " + out + " = " + map_expr(n.op, a[0], a[1], a[2]) + ";");
+        if (n.op == SANIC_OP_ROUND_Q8)   // the value a Q8 store + load gives (emit_metal.rs:100-103)
+            code.line("const float " + out + " = (float)sanic_to_q8(" + a[0] + ", " + flit(n.value) + ") * " + flit(n.value) + ";");
+        else
+            code.line("const float " + out + " = " + map_expr(n.op, a[0], a[1], a[2]) + ";");
         break;
     }
     case SANIC_NODE_SCAN: {
@@ -604,7 +617,13 @@ std::string Renderer::expr(Code& code, int e, const std::string& item, const std
     return out;
 }
 
-std::string store_stmt(const std::string& ptr, const std::string& idx, int dt, const std::string& v, bool coherent) {
+std::string store_stmt(const std::string& ptr, const std::string& idx, int dt, const std::string& v, bool coherent, double scale) {
+    if (dt == SANIC_Q8) {
+        // quantize at the store, clamped to the signed grid (emit_metal.rs:182-185, 226-229)
+        if (!(scale > 0.0)) fail(SANIC_ERR_DTYPE, "Q8 store without a positive scale");
+        const std::string q = "sanic_to_q8(" + v + ", " + flit(scale) + ")";
+        return coherent ? "sanic_st(" + ptr + " + " + idx + ", " + q + ");" : ptr + "[" + idx + "] = " + q + ";";
+    }
     if (coherent) {
         switch (dt) {
         case SANIC_F32: return "sanic_st(" + ptr + " + " + idx + ", (float)(" + v + "));";
@@ -833,7 +852,7 @@ static void emit_finish(Renderer& R, Code& code, const sanic_stage& st, const st
         v = R.value(code, st.epilogue, gc);
         R.memo.pop_back();
     }
-    code.line(store_stmt(R.param(st.out_buffer), gid, st.out_dtype, v));
+    code.line(store_stmt(R.param(st.out_buffer), gid, st.out_dtype, v, false, R.d->buffers[st.out_buffer].scale));
 }
 
 LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& scratch, const std::vector<int>& tails) {
@@ -1098,7 +1117,7 @@ LoweredStage lower_pointwise(const sanic_program_desc* d, int si) {
         body.line("if (" + w + " == 0.0f) return;");
     }
     std::string v = at(st.value);
-    body.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v));
+    body.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v, false, d->buffers[st.out_buffer].scale));
     std::ostringstream src;
     src << kPrelude << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(256) sanic_pointwise(Args a) {\n"
         << R.entry() << body.str() << "}\n";
@@ -1107,20 +1126,47 @@ LoweredStage lower_pointwise(const sanic_program_desc* d, int si) {
     return L;
 }
 
+// Does the stage read or write a Q8 buffer? The hand-written skeletons load and store only the
+// float, bf16 and nibble formats; such stages take the generic renderer.
+static bool stage_touches_q8(const sanic_program_desc* d, int s) {
+    const sanic_stage& st = d->stages[s];
+    if (d->buffers[st.out_buffer].dtype == SANIC_Q8) return true;
+    std::vector<int> todo;
+    if (st.kind == SANIC_STAGE_FUSED) {
+        for (int l = 0; l < st.n_leaves; l++) todo.push_back(st.leaf[l]);
+        if (st.epilogue >= 0) todo.push_back(st.epilogue);
+    } else {
+        todo.push_back(st.value);
+        if (st.where >= 0) todo.push_back(st.where);
+    }
+    while (!todo.empty()) {
+        const sanic_node& n = d->nodes[todo.back()];
+        todo.pop_back();
+        if (n.kind == SANIC_NODE_INPUT && n.dtype == SANIC_Q8) return true;
+        if (n.kind == SANIC_NODE_MAP && n.op == SANIC_OP_ROUND_Q8) return true;
+        if (n.kind != SANIC_NODE_INPUT)
+            for (int k = 0; k < n.n_in; k++) todo.push_back(n.in[k]);
+    }
+    return false;
+}
+
 Lowered lower_program(const sanic_program_desc* d) {
     validate(d);
     Lowered out;
     for (int s = 0; s < d->n_stages;) {
         const sanic_stage& st = d->stages[s];
+        // skeletons may batch or absorb the next few stages: none of them may touch Q8 either
+        bool generic = getenv("SANIC_HIP_GENERIC") != nullptr;
+        for (int t = s; t < std::min(d->n_stages, s + 8) && !generic; t++) generic = stage_touches_q8(d, t);
         if (st.kind == SANIC_STAGE_FUSED) {
             std::vector<LoweredStage> grp;
-            if (!getenv("SANIC_HIP_GENERIC") && lower_gemv_group(d, s, out.scratch_bytes, grp)) {
+            if (!generic && lower_gemv_group(d, s, out.scratch_bytes, grp)) {
                 for (auto& g : grp) out.stages.push_back(std::move(g));
                 s += (int)grp.size();
                 continue;
             }
             LoweredStage L;
-            if (!getenv("SANIC_HIP_GENERIC") && lower_skeleton(d, s, out.scratch_bytes, L)) {
+            if (!generic && lower_skeleton(d, s, out.scratch_bytes, L)) {
                 out.stages.push_back(std::move(L));
                 s++;
                 continue;
@@ -1131,7 +1177,7 @@ Lowered lower_program(const sanic_program_desc* d) {
             int64_t gv = 1;
             for (int j = 0; j < st.rank; j++) gv *= st.grid[j];
             if (st.sched.lane_stream && st.sched.split > 1 && std::min<int64_t>(st.sched.split, st.stream) > 1 && gv <= 4096)
-                for (int t = s + 1; tail_candidate(d, t) && tails.size() < 4; t++) tails.push_back(t);
+                for (int t = s + 1; tail_candidate(d, t) && !stage_touches_q8(d, t) && tails.size() < 4; t++) tails.push_back(t);
             L = lower_generic_fold(d, s, out.scratch_bytes, tails);
             out.stages.push_back(std::move(L));
             for (size_t t = 0; t < tails.size(); t++) {
@@ -1142,14 +1188,14 @@ Lowered lower_program(const sanic_program_desc* d) {
             s += (int)tails.size();
         } else {
             LoweredStage L;
-            int ab = getenv("SANIC_HIP_GENERIC") ? -1 : attn_absorber(d, s);
+            int ab = generic ? -1 : attn_absorber(d, s);
             if (ab >= 0) {
                 L.kernel_kind = "absorbed-into:" + std::to_string(ab);
                 out.stages.push_back(std::move(L));
                 s++;
                 continue;
             }
-            if (getenv("SANIC_HIP_GENERIC") || !lower_pointwise_skeleton(d, s, out.scratch_bytes, L))
+            if (generic || !lower_pointwise_skeleton(d, s, out.scratch_bytes, L))
                 L = lower_pointwise(d, s);
             out.stages.push_back(std::move(L));
         }

@@ -6,6 +6,7 @@
 
 #include <dlfcn.h>
 #include <sys/stat.h>
+#include <utime.h>
 #include <unistd.h>
 
 #include <cstring>
@@ -72,7 +73,10 @@ std::string compile_source(const std::string& generated) {
     std::string dir = cache_dir();
     std::string path = dir + "/" + hex + ".co";
     std::string code;
-    if (!getenv("SANIC_HIP_NO_CACHE") && read_file(path, code)) return code;
+    if (!getenv("SANIC_HIP_NO_CACHE") && read_file(path, code)) {
+        utime(path.c_str(), nullptr);   // mark as in use (the build prunes entries it did not touch)
+        return code;
+    }
 
     static std::mutex create_mu;
     hiprtcProgram prog;

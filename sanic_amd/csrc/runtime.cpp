@@ -94,8 +94,9 @@ __global__ void sanic_zero_words(uint32_t* p, int64_t n) {
     for (; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = 0u;
 }
 
-__device__ float load_as_float(const void* p, int dt, int64_t i) {
+__device__ float load_as_float(const void* p, int dt, float scale, int64_t i) {
     switch (dt) {
+    case SANIC_Q8: return (float)((const int8_t*)p)[i] * scale;
     case SANIC_F32: return ((const float*)p)[i];
     case SANIC_BF16: return __uint_as_float(((uint32_t)((const uint16_t*)p)[i]) << 16);
     case SANIC_U32: return (float)((const uint32_t*)p)[i];
@@ -104,8 +105,9 @@ __device__ float load_as_float(const void* p, int dt, int64_t i) {
     }
 }
 
-__device__ void store_from_float(void* p, int dt, int64_t i, float v) {
+__device__ void store_from_float(void* p, int dt, float scale, int64_t i, float v) {
     switch (dt) {
+    case SANIC_Q8: ((int8_t*)p)[i] = (int8_t)__builtin_fminf(__builtin_fmaxf(__builtin_rintf(v / scale), -127.0f), 127.0f); break;
     case SANIC_F32: ((float*)p)[i] = v; break;
     case SANIC_BF16: {
         uint32_t b = __float_as_uint(v);
@@ -119,9 +121,9 @@ __device__ void store_from_float(void* p, int dt, int64_t i, float v) {
     }
 }
 
-__global__ void sanic_convert(const void* src, int sdt, void* dst, int ddt, int64_t n) {
+__global__ void sanic_convert(const void* src, int sdt, float sscale, void* dst, int ddt, float dscale, int64_t n) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) store_from_float(dst, ddt, i, load_as_float(src, sdt, i));
+    if (i < n) store_from_float(dst, ddt, dscale, i, load_as_float(src, sdt, sscale, i));
 }
 
 // ── helpers ──────────────────────────────────────────────────────────────────────────────
@@ -511,6 +513,9 @@ int sanic_hip_capture(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int
             for (int k = 0; k < ob.rank; k++) no *= ob.shape[k];
             for (int k = 0; k < ib.rank; k++) ni *= ib.shape[k];
             if (no != ni) fail(SANIC_ERR_FEEDBACK, "feedback pair volumes differ (RunError::Feedback)");
+            for (int dt : {exe->buffers[o].dtype, exe->buffers[i].dtype})
+                if (dt != SANIC_F32 && dt != SANIC_BF16 && dt != SANIC_F16 && dt != SANIC_U32 && dt != SANIC_Q8)
+                    fail(SANIC_ERR_FEEDBACK, "feedback between unconvertible storage dtypes");
             rp->feedback.push_back({o, i});
         }
         hipStream_t s = exe->dev->stream;
@@ -523,8 +528,8 @@ int sanic_hip_capture(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int
                 int64_t n = 1;
                 for (int k = 0; k < ob.rank; k++) n *= ob.shape[k];
                 hipLaunchKernelGGL(sanic_convert, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                                   (const void*)rp->bound[fb.first]->ptr(), ob.dtype, (void*)rp->bound[fb.second]->ptr(),
-                                   ib.dtype, n);
+                                   (const void*)rp->bound[fb.first]->ptr(), ob.dtype, ob.scale,
+                                   (void*)rp->bound[fb.second]->ptr(), ib.dtype, ib.scale, n);
             }
         } catch (...) {
             hipGraph_t g;
@@ -598,7 +603,8 @@ int sanic_hip_step_many(sanic_hip_replay* rp, int n, double* gpu_seconds) {
                 int64_t cnt = 1;
                 for (int k = 0; k < ob.rank; k++) cnt *= ob.shape[k];
                 hipLaunchKernelGGL(sanic_convert, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, s,
-                                   (const void*)rp->bound[fb.first]->ptr(), ob.dtype, (void*)rp->bound[fb.second]->ptr(), ib.dtype, cnt);
+                                   (const void*)rp->bound[fb.first]->ptr(), ob.dtype, ob.scale,
+                                   (void*)rp->bound[fb.second]->ptr(), ib.dtype, ib.scale, cnt);
             }
             SANIC_HIP(hipStreamSynchronize(s));
         }

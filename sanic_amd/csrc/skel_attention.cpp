@@ -457,7 +457,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         R.memo.pop_back();
         k.line("float " + nm + "val = " + val + ";");
         k.line("if (" + cond + " != 0.0f) {");
-        k.line("  " + store_stmt(R.param(w.buffer), "wf", d->buffers[w.buffer].dtype, nm + "val"));
+        k.line("  " + store_stmt(R.param(w.buffer), "wf", d->buffers[w.buffer].dtype, nm + "val", false, d->buffers[w.buffer].scale));
         if (d->buffers[w.buffer].dtype == SANIC_BF16) k.line("  " + nm + "val = __uint_as_float((unsigned)sanic_to_bf16(" + nm + "val) << 16);");
         k.line("} else {");
         k.line("  " + nm + "val = " + (w.is_k ? std::string("sanic_bf16(kp[") + nm + "row * " + std::to_string(kt) + " + xw])"
@@ -887,7 +887,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         v = R.value(k, st.epilogue, gc);
     }
     R.memo.pop_back();
-    k.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v));
+    k.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v, false, d->buffers[st.out_buffer].scale));
     k.indent--;
     k.line("}");
     k.indent--;

@@ -321,7 +321,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         std::string lin;
         for (int j = 0; j < st.rank; j++)
             lin = j == 0 ? "(idx_t)(" + gc[0] + ")" : "(" + lin + " * " + std::to_string(st.grid[j]) + " + (idx_t)(" + gc[j] + "))";
-        fo.line(store_stmt(Ro.param(st.out_buffer), lin, st.out_dtype, v));
+        fo.line(store_stmt(Ro.param(st.out_buffer), lin, st.out_dtype, v, false, d->buffers[st.out_buffer].scale));
     }
     for (int b : Ro.bufs) R.param(b);
     std::string qp = R.param(P.qacc.buffer), kp = R.param(P.kacc.buffer), vp = R.param(P.vacc.buffer);

@@ -669,7 +669,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     std::string lin;
     for (int j = 0; j < st.rank; j++)
         lin = j == 0 ? "(idx_t)(" + gc[0] + ")" : "(" + lin + " * " + std::to_string(st.grid[j]) + " + (idx_t)(" + gc[j] + "))";
-    k.line(store_stmt(R.param(st.out_buffer), lin, st.out_dtype, v));
+    k.line(store_stmt(R.param(st.out_buffer), lin, st.out_dtype, v, false, d->buffers[st.out_buffer].scale));
     k.indent -= 3;
     k.line("    }");
 

@@ -462,7 +462,7 @@ static std::string gemv_finish(Renderer& R, Code& code, const sanic_program_desc
         v = R.value(code, st.epilogue, gc);
         R.memo.pop_back();
     }
-    code.line(store_stmt(R.param(st.out_buffer), "nn", st.out_dtype, v, coherent));
+    code.line(store_stmt(R.param(st.out_buffer), "nn", st.out_dtype, v, coherent, d->buffers[st.out_buffer].scale));
     return v;
 }
 
@@ -570,7 +570,7 @@ void emit_pointwise_loop(Renderer& R, Code& body, const sanic_program_desc* d, i
         body.line("if (" + w + " == 0.0f) continue;");
     }
     std::string v = at(st.value);
-    body.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v));
+    body.line(store_stmt(R.param(st.out_buffer), "gid", st.out_dtype, v, false, d->buffers[st.out_buffer].scale));
     R.memo.pop_back();
     body.indent--;
     body.line("}");
@@ -933,7 +933,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
             std::string pv = R.value(k, pst.value, {"wi"});
             R.memo.pop_back();
             R.subst.clear();
-            k.line(store_stmt(R.param(pst.out_buffer), "wi", pst.out_dtype, pv, !tails.empty()));
+            k.line(store_stmt(R.param(pst.out_buffer), "wi", pst.out_dtype, pv, !tails.empty(), d->buffers[pst.out_buffer].scale));
             k.indent--;
             k.line("}");
         } else {
@@ -1119,7 +1119,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
             std::string pv = R.value(c, pst.value, {"wi"});
             R.memo.pop_back();
             R.subst.clear();
-            c.line(store_stmt(R.param(pst.out_buffer), "wi", pst.out_dtype, pv, !tails.empty()));
+            c.line(store_stmt(R.param(pst.out_buffer), "wi", pst.out_dtype, pv, !tails.empty(), d->buffers[pst.out_buffer].scale));
             c.indent--;
             c.line("}");
             return;

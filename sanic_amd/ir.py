@@ -13,29 +13,58 @@ argmax, silu) restate the graph *semantics* of /root/reference/src/ir.rs:1171-15
 from __future__ import annotations
 
 import math
+
+import numpy as np
 from dataclasses import dataclass, field
 from typing import List, Optional, Sequence, Tuple
 
 # storage dtypes (include/sanic_hip.h)
-F64, F32, F16, BF16, U32, I8, I4, U4 = range(8)
-DTYPE_NAMES = {F64: "f64", F32: "f32", F16: "f16", BF16: "bf16", U32: "u32", I8: "i8", I4: "i4", U4: "u4"}
+F64, F32, F16, BF16, U32, I8, I4, U4, Q8 = range(9)
+DTYPE_NAMES = {F64: "f64", F32: "f32", F16: "f16", BF16: "bf16", U32: "u32", I8: "i8", I4: "i4", U4: "u4",
+               Q8: "q8"}
+
+
+class Q8Dtype(int):
+    """`Dtype::Q8 { scale }` (/root/reference/src/scalar.rs:190-198, `Dtype::q8` :276-282): the
+    storage code Q8 with its grid step riding along — the scale is part of the type."""
+
+    def __new__(cls, scale: float):
+        obj = super().__new__(cls, Q8)
+        obj.scale = float(np.float32(scale))
+        return obj
+
+    def __repr__(self):
+        return f"q8({self.scale})"
+
+
+def q8(scale: float) -> Q8Dtype:
+    if not scale > 0:
+        raise ValueError("a Q8 grid needs a positive scale")
+    return Q8Dtype(scale)
+
+
+def dtype_scale(dt: int) -> float:
+    """The quantization scale of a dtype that has one (scalar.rs:284-289), else 0."""
+    return float(getattr(dt, "scale", 0.0))
 
 
 def dtype_bytes(dt: int, n: int) -> int:
     """Bytes of `n` packed elements of storage dtype `dt`."""
     if dt in (I4, U4):
         return (n + 1) // 2
-    return n * {F64: 8, F32: 4, F16: 2, BF16: 2, U32: 4, I8: 1}[dt]
+    return n * {F64: 8, F32: 4, F16: 2, BF16: 2, U32: 4, I8: 1, Q8: 1}[int(dt)]
 
 
 # MapOp codes (/root/reference/src/scalar.rs:45-69)
 (ADD, SUB, MUL, DIV, MAX, MIN, LT, NEG, RECIP, EXP, LOG, SQRT, TANH, SIN, COS, WHERE,
- ROUND_BF16, ROUND_F32) = range(18)
+ ROUND_BF16, ROUND_F32, ROUND_Q8) = range(19)
 ARITY = {ADD: 2, SUB: 2, MUL: 2, DIV: 2, MAX: 2, MIN: 2, LT: 2, NEG: 1, RECIP: 1, EXP: 1,
-         LOG: 1, SQRT: 1, TANH: 1, SIN: 1, COS: 1, WHERE: 3, ROUND_BF16: 1, ROUND_F32: 1}
+         LOG: 1, SQRT: 1, TANH: 1, SIN: 1, COS: 1, WHERE: 3, ROUND_BF16: 1, ROUND_F32: 1,
+         ROUND_Q8: 1}
 OP_NAMES = {ADD: "+", SUB: "-", MUL: "·", DIV: "/", MAX: "max", MIN: "min", LT: "<", NEG: "neg",
             RECIP: "recip", EXP: "exp", LOG: "log", SQRT: "sqrt", TANH: "tanh", SIN: "sin",
-            COS: "cos", WHERE: "where", ROUND_BF16: "round_bf16", ROUND_F32: "round_f32"}
+            COS: "cos", WHERE: "where", ROUND_BF16: "round_bf16", ROUND_F32: "round_f32",
+            ROUND_Q8: "round_q8"}
 
 # Monoids (/root/reference/src/scalar.rs:18-41)
 M_ADD, M_MUL, M_MAX, M_MIN, M_LSE = range(5)
@@ -123,6 +152,20 @@ def map_(op: int, *ins: Node) -> Node:
     if len(ins) != ARITY[op]:
         raise ValueError(f"map op {OP_NAMES[op]} takes {ARITY[op]} inputs")
     return Node(MAP, broadcast_shape([i.shape for i in ins]), ins, op=op)
+
+
+def round_to(src: Node, dtype: int) -> Node:
+    """MapOp::RoundTo(dtype) (scalar.rs:120-152, emit_metal.rs:95-104): the value a store at
+    that width followed by a load gives. Q8 carries its scale in the node's `value`."""
+    if int(dtype) == Q8:
+        return Node(MAP, src.shape, (src,), op=ROUND_Q8, value=dtype_scale(dtype))
+    if dtype == BF16:
+        return map_(ROUND_BF16, src)
+    if dtype == F32:
+        return map_(ROUND_F32, src)
+    if dtype == F64:
+        return src
+    raise ValueError(f"RoundTo({DTYPE_NAMES.get(int(dtype), dtype)}) needs a scale, not a plain rounding")
 
 
 def reduce(src: Node, dim: int, monoid: int) -> Node:

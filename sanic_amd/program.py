@@ -196,6 +196,7 @@ class Program:
         for i, b in enumerate(self.buffers):
             bufs[i]["role"] = b.role
             bufs[i]["dtype"] = b.dtype
+            bufs[i]["scale"] = ir.dtype_scale(b.dtype)
             bufs[i]["rank"] = len(b.shape)
             bufs[i]["shape"] = list(b.shape) + [0] * (abi.MAX_RANK - len(b.shape))
         keep = [nodes, exprs, reindex, bufs, stages]
