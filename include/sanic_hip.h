@@ -63,14 +63,15 @@ enum {
     SANIC_I8 = 5, SANIC_I4 = 6, SANIC_U4 = 7, SANIC_Q8 = 8
 };
 
-/* MapOp (/root/reference/src/scalar.rs:45-69). ROUND_BF16/ROUND_F32 are `RoundTo(dtype)`;
- * ROUND_Q8 is `RoundTo(Q8 { scale })` with the scale in the MAP node's `value`
- * (emit_metal.rs:100-103: the value a Q8 store+load would give); nodes only, not carrier Exprs. */
+/* MapOp (/root/reference/src/scalar.rs:45-69). ROUND_BF16/ROUND_F32/ROUND_F16 are
+ * `RoundTo(dtype)`; ROUND_Q8 is `RoundTo(Q8 { scale })` with the scale in the MAP node's `value`
+ * (emit_metal.rs:95-104: the value a store + load at that width would give). ROUND_Q8 and
+ * ROUND_F16 are node ops only, not carrier Expr ops. */
 enum {
     SANIC_OP_ADD = 0, SANIC_OP_SUB, SANIC_OP_MUL, SANIC_OP_DIV, SANIC_OP_MAX, SANIC_OP_MIN,
     SANIC_OP_LT, SANIC_OP_NEG, SANIC_OP_RECIP, SANIC_OP_EXP, SANIC_OP_LOG, SANIC_OP_SQRT,
     SANIC_OP_TANH, SANIC_OP_SIN, SANIC_OP_COS, SANIC_OP_WHERE, SANIC_OP_ROUND_BF16,
-    SANIC_OP_ROUND_F32, SANIC_OP_ROUND_Q8
+    SANIC_OP_ROUND_F32, SANIC_OP_ROUND_Q8, SANIC_OP_ROUND_F16
 };
 
 /* Monoid (/root/reference/src/scalar.rs:18-41). */

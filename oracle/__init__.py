@@ -36,6 +36,8 @@ def lib():
         L.oracle_round_bf16.argtypes = [ctypes.c_double]
         L.oracle_round_to.restype = ctypes.c_double
         L.oracle_round_to.argtypes = [ctypes.c_int, ctypes.c_double]
+        L.oracle_round_f16.restype = ctypes.c_double
+        L.oracle_round_f16.argtypes = [ctypes.c_double]
         L.oracle_round_q8.restype = ctypes.c_double
         L.oracle_round_q8.argtypes = [ctypes.c_double, ctypes.c_double]
         L.oracle_eval.argtypes = [VP, ctypes.c_int, VP, VP]
@@ -84,6 +86,11 @@ def f64(a) -> np.ndarray:
 
 def round_bf16(v: float) -> float:
     return lib().oracle_round_bf16(float(v))
+
+
+def round_f16(v: float) -> float:
+    """round_to(F16, v) (scalar.rs:124-127, 154-178)."""
+    return lib().oracle_round_f16(float(v))
 
 
 def round_q8(scale: float, v: float) -> float:

@@ -54,11 +54,30 @@ double oracle_round_q8(double scale, double v) {
     return q * scale;
 }
 
+/* scalar.rs:154-178 semantics (f64 → f32 → IEEE half → f32, ties to even, overflow to ±∞,
+   half subnormals on the 2^-24 grid), restated as "round to the half ulp of the value's binade":
+   the ulp is 2^(e−10) for |x| in [2^e, 2^(e+1)), never below 2^-24 */
+double oracle_round_f16(double v) {
+    float f = (float)v;
+    if (isnan(f) || isinf(f)) return (double)f;
+    double m = fabs((double)f);
+    if (m == 0.0) return (double)f;
+    int e;
+    frexp(m, &e);                       /* m in [2^(e−1), 2^e) */
+    int ue = e - 1 - 10;
+    if (ue < -24) ue = -24;
+    double q = nearbyint(ldexp(m, -ue)); /* default rounding mode: ties to even */
+    double r = ldexp(q, ue);
+    if (r > 65504.0) r = INFINITY;
+    return f < 0 ? -r : r;
+}
+
 double oracle_round_to(int dtype, double v) {
     switch (dtype) {
     case SANIC_F64: return v;
     case SANIC_F32: return (double)(float)v;
     case SANIC_BF16: return oracle_round_bf16(v);
+    case SANIC_F16: return oracle_round_f16(v);
     case SANIC_U32: {
         /* the saturating u32 store (emit_metal.rs:186-190): computed in f32 */
         float f = (float)v;
@@ -90,6 +109,7 @@ double oracle_apply_map(int op, const double* a) {
     case SANIC_OP_WHERE: return a[0] != 0.0 ? a[1] : a[2];
     case SANIC_OP_ROUND_BF16: return oracle_round_bf16(a[0]);
     case SANIC_OP_ROUND_F32: return (double)(float)a[0];
+    case SANIC_OP_ROUND_F16: return oracle_round_f16(a[0]);
     }
     return NAN;
 }

@@ -21,6 +21,7 @@ extern "C" {
 double oracle_round_bf16(double v);
 double oracle_round_to(int dtype, double v);
 double oracle_round_q8(double scale, double v);
+double oracle_round_f16(double v);
 double oracle_apply_map(int op, const double* a);
 double oracle_monoid_identity(int m);
 double oracle_monoid_combine(int m, double a, double b);

@@ -74,7 +74,7 @@ static void check_node(const sanic_program_desc* d, int i) {
     case SANIC_NODE_FOLD: break;
     case SANIC_NODE_MAP: {
         int ar = (n.op == SANIC_OP_WHERE) ? 3 : (n.op <= SANIC_OP_LT ? 2 : 1);
-        if (n.op < 0 || n.op > SANIC_OP_ROUND_Q8 || n.n_in != ar) bad("map arity");
+        if (n.op < 0 || n.op > SANIC_OP_ROUND_F16 || n.n_in != ar) bad("map arity");
         if (n.op == SANIC_OP_ROUND_Q8 && !(n.value > 0.0)) bad("Q8 rounding needs a positive scale");
         for (int k = 0; k < n.n_in; k++) {
             const sanic_node& c = child(k);
@@ -333,6 +333,7 @@ std::string map_expr(int op, const std::string& a, const std::string& b, const s
     case SANIC_OP_WHERE: return "((" + a + " != 0.0f) ? " + b + " : " + c + ")";
     case SANIC_OP_ROUND_BF16: return "sanic_round_bf16(" + a + ")";
     case SANIC_OP_ROUND_F32: return "(" + a + ")";
+    case SANIC_OP_ROUND_F16: return "((float)(_Float16)(" + a + "))";
     }
     fail(SANIC_ERR_COMPILE, "unknown map op");
 }

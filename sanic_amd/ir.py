@@ -57,14 +57,14 @@ def dtype_bytes(dt: int, n: int) -> int:
 
 # MapOp codes (/root/reference/src/scalar.rs:45-69)
 (ADD, SUB, MUL, DIV, MAX, MIN, LT, NEG, RECIP, EXP, LOG, SQRT, TANH, SIN, COS, WHERE,
- ROUND_BF16, ROUND_F32, ROUND_Q8) = range(19)
+ ROUND_BF16, ROUND_F32, ROUND_Q8, ROUND_F16) = range(20)
 ARITY = {ADD: 2, SUB: 2, MUL: 2, DIV: 2, MAX: 2, MIN: 2, LT: 2, NEG: 1, RECIP: 1, EXP: 1,
          LOG: 1, SQRT: 1, TANH: 1, SIN: 1, COS: 1, WHERE: 3, ROUND_BF16: 1, ROUND_F32: 1,
-         ROUND_Q8: 1}
+         ROUND_Q8: 1, ROUND_F16: 1}
 OP_NAMES = {ADD: "+", SUB: "-", MUL: "·", DIV: "/", MAX: "max", MIN: "min", LT: "<", NEG: "neg",
             RECIP: "recip", EXP: "exp", LOG: "log", SQRT: "sqrt", TANH: "tanh", SIN: "sin",
             COS: "cos", WHERE: "where", ROUND_BF16: "round_bf16", ROUND_F32: "round_f32",
-            ROUND_Q8: "round_q8"}
+            ROUND_Q8: "round_q8", ROUND_F16: "round_f16"}
 
 # Monoids (/root/reference/src/scalar.rs:18-41)
 M_ADD, M_MUL, M_MAX, M_MIN, M_LSE = range(5)
@@ -163,6 +163,8 @@ def round_to(src: Node, dtype: int) -> Node:
         return map_(ROUND_BF16, src)
     if dtype == F32:
         return map_(ROUND_F32, src)
+    if dtype == F16:
+        return map_(ROUND_F16, src)
     if dtype == F64:
         return src
     raise ValueError(f"RoundTo({DTYPE_NAMES.get(int(dtype), dtype)}) needs a scale, not a plain rounding")

@@ -96,3 +96,32 @@ def test_library_refuses_a_q8_grid_without_scale():
     keep[3][0]["scale"] = 0.0               # a Q8 buffer whose scale was never set
     assert abi.lib().sanic_hip_precompile(ctypes.byref(desc)) != 0
     assert b"scale" in abi.lib().sanic_hip_last_error()
+
+
+def test_round_f16_matches_numpy_half_conversion():
+    """round_to(F16) (scalar.rs:154-178: ties to even, overflow to ±∞, subnormals on the 2^-24
+    grid) against numpy's own f32 → f16 conversion, over edge values and a random sweep."""
+    edge = [0.0, -0.0, 1.0, 65504.0, 65519.99, 65520.0, 1e6, -1e6, 2.0 ** -24, 2.0 ** -25,
+            3 * 2.0 ** -26, 2.0 ** -14, 2.0 ** -14 - 2.0 ** -25, 1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11,
+            0.1, -0.3333, float("inf"), float("-inf")]
+    rng = np.random.default_rng(5)
+    sweep = np.concatenate([rng.standard_normal(4000) * 10.0 ** rng.integers(-9, 6, 4000)])
+    for v in edge + sweep.tolist():
+        with np.errstate(over="ignore"):
+            want = float(np.float32(v).astype(np.float16))
+        got = oracle.round_f16(v)
+        assert got == want or (np.isnan(got) and np.isnan(want)), (v, got, want)
+    assert np.isnan(oracle.round_f16(float("nan")))
+
+
+def test_f16_output_store_is_narrowed_by_the_oracle():
+    p = Program()
+    x = p.input("X", (5,), ir.F32)
+    p.pointwise("Y", ir.round_to(x, ir.F16) - x, ir.F32)
+    p.pointwise("Z", x * 1.0, ir.F16)
+    vals = np.array([0.1, 1 + 2.0 ** -11, 70000.0, 2.0 ** -25, -3.3])
+    out = oracle.run_program(p, {"X": vals})
+    with np.errstate(over="ignore"):
+        want = np.float32(vals).astype(np.float16).astype(np.float64)
+    assert out["Z"].tolist() == want.tolist()
+    np.testing.assert_array_equal(out["Y"], (want - vals).astype(np.float32).astype(np.float64))   # Y is stored f32

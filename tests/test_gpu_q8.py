@@ -1,6 +1,7 @@
-"""Q8 storage on the GPU through the C ABI against the oracle: the pinned-output grid
-(/root/reference/tests/metal.rs:2402-2446, equality, no tolerance), dequantizing loads in a
-fold, RoundTo(Q8) inside a stage, a split fold stored to Q8, and a Q8 feedback input."""
+"""Narrow storage on the GPU through the C ABI against the oracle: Q8 (the pinned-output grid
+of /root/reference/tests/metal.rs:2402-2446, equality, no tolerance; dequantizing loads in a
+fold; RoundTo(Q8) inside a stage; a split fold stored to Q8; a Q8 feedback input) and F16
+(RoundTo(F16) and an F16-stored output)."""
 import numpy as np
 import pytest
 
@@ -82,3 +83,19 @@ def test_feedback_into_a_q8_input(dev):
     for _ in range(3):
         rp.step()
     np.testing.assert_array_equal(xb.read(p.by_name["x"].dtype, 8), x0 + 0.75)
+
+
+def test_round_to_f16_and_f16_store(dev):
+    """RoundTo(F16) inside a stage and an F16-stored output on the GPU against the oracle's
+    half rounding (ties to even, overflow to ∞, subnormals): exact."""
+    p = Program()
+    x = p.input("X", (1024,), ir.F32)
+    p.pointwise("Y", ir.round_to(x, ir.F16) * 2.0, ir.F32)
+    p.pointwise("Z", x * 1.0, ir.F16)
+    v = oracle.lcg(1616, 1024) * 10.0 ** np.repeat(np.arange(-8, 8), 64)
+    v[:6] = [65519.0, 65520.0, -1e6, 2.0 ** -25, 3 * 2.0 ** -26, 1 + 2.0 ** -11]
+    vals = {"X": v}
+    got, _ = run_on_gpu(dev, p, vals)
+    want = oracle.run_program(p, vals)
+    assert got["Y"].tolist() == want["Y"].tolist()
+    assert got["Z"].tolist() == want["Z"].tolist()
