@@ -227,7 +227,10 @@ typedef struct sanic_program_desc {
     int32_t n_stages;         const sanic_stage* stages;
 } sanic_program_desc;
 
-/* DeviceSpecs (/root/reference/src/cost.rs:33-60), filled with MI355X figures. */
+/* DeviceSpecs (/root/reference/src/cost.rs:33-60), filled with MI355X figures. The last five
+ * fields are the cost model's own (cost.rs:40-50, used by kernel_time / sustainable_bandwidth,
+ * cost.rs:150-210): the Rust side's `Backend::specs` copies them into `DeviceSpecs` together
+ * with hbm_bytes_per_s (hbm_bandwidth) and bf16_mfma_flops (peak_flops). */
 typedef struct sanic_device_specs {
     char name[64];
     int32_t compute_units;
@@ -238,6 +241,11 @@ typedef struct sanic_device_specs {
     double f32_flops;
     double clock_hz;
     int64_t hbm_bytes;
+    double sram_bytes;          /* LDS one workgroup may allocate (160 KiB on gfx950)          */
+    double regfile_bytes;       /* vector registers of one CU (4 SIMDs × 128 KiB)             */
+    double launch_overhead_s;   /* measured floor of a dependent kernel launch in a hipGraph  */
+    double min_blocks;          /* workgroups that fill the chip: 2 per CU                    */
+    double mem_latency_s;       /* loaded HBM latency (Little's law: ≈16 MB in flight at 8 TB/s) */
 } sanic_device_specs;
 
 typedef struct sanic_hip_device sanic_hip_device;

@@ -66,7 +66,9 @@ class DeviceSpecs(ctypes.Structure):
         ("wave_size", ctypes.c_int32), ("lds_bytes_per_cu", ctypes.c_int32),
         ("hbm_bytes_per_s", ctypes.c_double), ("bf16_mfma_flops", ctypes.c_double),
         ("f32_flops", ctypes.c_double), ("clock_hz", ctypes.c_double),
-        ("hbm_bytes", ctypes.c_int64),
+        ("hbm_bytes", ctypes.c_int64), ("sram_bytes", ctypes.c_double),
+        ("regfile_bytes", ctypes.c_double), ("launch_overhead_s", ctypes.c_double),
+        ("min_blocks", ctypes.c_double), ("mem_latency_s", ctypes.c_double),
     ]
 
 

@@ -85,3 +85,16 @@ def test_c3_decode_attention_split(dev, pos):
     print(exe.stage_kernel(0), pos, bf16_rel(got["o"], want))
     assert exe.stage_kernel(0).startswith("skeleton:attn_decode")
     assert bf16_rel(got["o"], want) < 2e-2
+
+
+def test_device_specs_carry_the_cost_model_fields(dev):
+    """Backend::specs (compile.rs:87-108) → DeviceSpecs (cost.rs:33-60): the MI355X figures
+    the reference's cost model reads, plus the hardware facts from the runtime."""
+    s = dev.specs()
+    assert s.compute_units == 256 and s.wave_size == 64
+    assert s.hbm_bytes > 250 * 2 ** 30
+    assert s.hbm_bytes_per_s == 8.0e12 and s.bf16_mfma_flops == 2.5e15
+    assert s.sram_bytes == 160 * 1024 and s.regfile_bytes == 512 * 1024
+    assert s.launch_overhead_s == 2.6e-6 and s.min_blocks == 2 * s.compute_units
+    # Little's law at these figures: the decode GEMV's 33.5 MB in flight saturates HBM
+    assert 33.5e6 / (s.hbm_bytes_per_s * s.mem_latency_s) >= 1.0
