@@ -1272,7 +1272,8 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     // a 128-byte line are read through the same L2.
     int SW = 32;                                  // strip width (columns); 64 measured slower
     if (const char* e = getenv("SANIC_GEMVT_SW")) SW = atoi(e) <= 32 ? 32 : 64;
-    const int NT = SW == 64 ? 512 : 256;          // 32 row loads per lane either way
+    int NT = 512;                                 // 8 waves: 16 (SW 32) / 32 (SW 64) row loads per lane
+    if (const char* e = getenv("SANIC_GEMVT_NT")) NT = atoi(e) >= 1024 ? 1024 : atoi(e) >= 512 ? 512 : 256;
     const int LPR = SW / 8, RPS = 64 / LPR, NWV = NT / 64;   // lanes per row, rows per step, waves
     if (N % (SW * 8) == 0 && K % (RPS * NWV) == 0 && K <= 8192 && !getenv("SANIC_GEMVT_SLICES")) {
         const int SC = (int)P.cslots.size(), SR = (int)P.rslots.size();
