@@ -291,6 +291,52 @@ template <class T> __device__ __forceinline__ T sanic_ld(const T* p) {
 template <class T> __device__ __forceinline__ void sanic_st(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Cross-lane reductions without the LDS pipe (__shfl_xor lowers to ds_bpermute, ~100 cycles a
+// step on a dependent chain): DPP within rows of 16 lanes — quad_perm [1,0,3,2] (lane ^ 1),
+// [2,3,0,1] (lane ^ 2), row_ror 4 / 8 — and the gfx950 permlane swaps across rows. After
+// permlane32_swap(v, v) the pair holds v[i mod 32] and v[i mod 32 + 32]; after
+// permlane16_swap(v, v) lanes of rows 2j and 2j+1 hold rows 2j and 2j+1.
+// (a lane whose source is disabled reads `fill`: 0 for sums, its own value for maxima)
+template <int C> __device__ __forceinline__ float sanic_dpp(float v, float fill = 0.0f) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(v), C, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float sanic_rows_sum(float v) {   // Σ over lanes i, i^16, i^32, i^48
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+}
+__device__ __forceinline__ float sanic_rows_max(float v) {
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __builtin_fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __builtin_fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+}
+__device__ __forceinline__ float sanic_quad_sum(float v) {   // Σ over the 4 lanes of a quad
+  v += sanic_dpp<0xB1>(v);
+  return v + sanic_dpp<0x4E>(v);
+}
+__device__ __forceinline__ float sanic_wave_sum(float v) {   // Σ over all 64 lanes, in every lane
+  v = sanic_quad_sum(v);
+  v += sanic_dpp<0x124>(v);
+  v += sanic_dpp<0x128>(v);
+  return sanic_rows_sum(v);
+}
+__device__ __forceinline__ float sanic_wave_max(float v) {
+  v = __builtin_fmaxf(v, sanic_dpp<0xB1>(v, v));
+  v = __builtin_fmaxf(v, sanic_dpp<0x4E>(v, v));
+  v = __builtin_fmaxf(v, sanic_dpp<0x124>(v, v));
+  v = __builtin_fmaxf(v, sanic_dpp<0x128>(v, v));
+  return sanic_rows_max(v);
+}
+__device__ __forceinline__ float sanic_stride4_sum(float v) { // Σ over lanes ≡ i (mod 4)
+  v += sanic_dpp<0x124>(v);
+  v += sanic_dpp<0x128>(v);
+  return sanic_rows_sum(v);
+}
+__device__ __forceinline__ float sanic_stride8_sum(float v) { // Σ over lanes ≡ i (mod 8)
+  return sanic_rows_sum(v + sanic_dpp<0x128>(v));
+}
 __device__ __forceinline__ float sanic_lse(float a, float b) {
   if (a == -__builtin_huge_valf()) return b;
   if (b == -__builtin_huge_valf()) return a;

@@ -408,7 +408,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     bool lo_static = true;
     for (auto& b : win) lo_static &= b.kind != WindowBound::LO_CEIL;
     const std::string tpre = lo_static ? "((idx_t)chunk * " + std::to_string(CH) + ")" : "t0";
-    const int LPT = 4;                                   // lanes per key position
+    constexpr int LPT = 4;                               // lanes per key position
     const int64_t DPL = HD / LPT;                        // contiguous d per lane (multiple of 8)
     const int PPP = NT / LPT;                            // key positions per score pass
     const int NP = CH / PPP;                             // score passes
@@ -562,7 +562,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
             k.indent++;
             k.line("float dv = 0.0f;");
             k.line("for (int dd = lane; dd < " + std::to_string(HD) + "; dd += 64) dv = fmaf(q_lds[" + std::to_string(r * HD) + " + dd], knew_lds[dd], dv);");
-            k.line("for (int off = 32; off > 0; off >>= 1) dv += __shfl_xor(dv, off, 64);");
+            k.line("dv = sanic_wave_sum(dv);");
             k.line("if (lane == 0) {");
             k.indent++;
             k.line("const float dotv = dv;");
@@ -655,8 +655,8 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("}");
     k.line("#pragma unroll");
     k.line("for (int r = 0; r < " + std::to_string(REP) + "; ++r) {");
-    k.line("  #pragma unroll");
-    k.line("  for (int off = 1; off < " + std::to_string(LPT) + "; off <<= 1) dot[r] += __shfl_xor(dot[r], off, 64);");
+    static_assert(LPT == 4, "the score reduction is a quad sum");
+    k.line("  dot[r] = sanic_quad_sum(dot[r]);");
     k.line("}");
     k.line("if (sub == 0) {");
     k.indent++;
@@ -691,14 +691,14 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.indent++;
     k.line("float m = (-__builtin_huge_valf());");
     k.line("for (int i = lane; i < " + std::to_string(CH) + "; i += 64) m = fmaxf(m, p_lds[r][i]);");
-    k.line("for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));");
+    k.line("m = sanic_wave_max(m);");
     k.line("float l = 0.0f;");
     k.line("for (int i = lane; i < " + std::to_string(CH) + "; i += 64) {");
     k.line("  const float p = m == (-__builtin_huge_valf()) ? 0.0f : __builtin_amdgcn_exp2f((p_lds[r][i] - m) * 1.44269504088896341f);");
     k.line("  p_lds[r][i] = p;");
     k.line("  l += p;");
     k.line("}");
-    k.line("for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);");
+    k.line("l = sanic_wave_sum(l);");
     k.line("if (lane == 0) { stat_lds[r][0] = m; stat_lds[r][1] = l; }");
     k.indent--;
     k.line("}");
@@ -837,7 +837,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.indent++;
     k.line("float m = (-__builtin_huge_valf());");
     k.line("for (int ch = lane; ch < " + std::to_string(NPART) + "; ch += 64) m = fmaxf(m, g_lds[(ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + "]);");
-    k.line("for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));");
+    k.line("m = sanic_wave_max(m);");
     k.line("for (int ch = lane; ch < " + std::to_string(NPART) + "; ch += 64) {");
     k.line("  const float mc = g_lds[(ch * " + std::to_string(REP) + " + r) * " + std::to_string(PSZ) + "];");
     k.line("  w_lds[r][ch] = (-__builtin_huge_valf()) < mc ? __builtin_amdgcn_exp2f((mc - m) * 1.44269504088896341f) : 0.0f;");

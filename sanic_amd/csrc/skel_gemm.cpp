@@ -321,7 +321,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         }
         for (int i = 0; i < SR; i++) {
             std::string r = "rp" + std::to_string(i);
-            kp.line("for (int off = 32; off > 0; off >>= 1) " + r + " += __shfl_xor(" + r + ", off, 64);");
+            kp.line(r + " = sanic_wave_sum(" + r + ");");
             kp.line("if (lane == 0) ((float*)((char*)a.scratch + " + std::to_string(rs_off) + "))[mp * " + std::to_string(SR) + " + " + std::to_string(i) + "] = " + r + ";");
         }
     }
@@ -636,7 +636,9 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     if (SR && !pre) {
         for (int i = 0; i < SR; i++) {
             std::string r = "racc" + std::to_string(i);
-            for (int off = 1; off < TPR; off <<= 1) k.line(r + " += __shfl_xor(" + r + ", " + std::to_string(off) + ", 64);");
+            // TPR consecutive lanes (2 or 4) hold one row's partials: lane ^ 1, then lane ^ 2
+            k.line(r + " += sanic_dpp<0xB1>(" + r + ");");
+            if (TPR == 4) k.line(r + " += sanic_dpp<0x4E>(" + r + ");");
             k.line("if (tid % " + std::to_string(TPR) + " == 0) rs_lds[(tid / " + std::to_string(TPR) + ") * " + std::to_string(SR) + " + " + std::to_string(i) + "] = " + r + ";");
         }
         k.line("__syncthreads();");

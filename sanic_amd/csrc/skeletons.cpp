@@ -875,7 +875,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
             for (int cs = 0; cs < SC; cs++) parts.push_back("acc" + std::to_string(q) + "_" + std::to_string(cs));
         for (int r = 0; r < SR; r++) parts.push_back("rpart" + std::to_string(r));
         for (size_t i = 0; i < parts.size(); i++) {
-            k.line("for (int off = 32; off > 0; off >>= 1) " + parts[i] + " += __shfl_xor(" + parts[i] + ", off, 64);");
+            k.line(parts[i] + " = sanic_wave_sum(" + parts[i] + ");");
         }
         k.line("if (lane == 0) {");
         for (size_t i = 0; i < parts.size(); i++) k.line("  red[wv][" + std::to_string(i) + "] = " + parts[i] + ";");
@@ -1079,7 +1079,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
             for (int q = 0; q < RQ; q++)
                 for (int cs = 0; cs < SC; cs++) {
                     std::string a = "acc" + std::to_string(q) + "_" + std::to_string(cs);
-                    c.line("for (int off = 32; off > 0; off >>= 1) " + a + " += __shfl_xor(" + a + ", off, 64);");
+                    c.line(a + " = sanic_wave_sum(" + a + ");");
                 }
             c.line("if (lane == 0 && live0) {");
             c.indent++;
@@ -1127,7 +1127,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         for (int q = 0; q < RQ; q++)
             for (int cs = 0; cs < SC; cs++) {
                 std::string a = "acc" + std::to_string(q) + "_" + std::to_string(cs);
-                c.line("for (int off = 32; off > 0; off >>= 1) " + a + " += __shfl_xor(" + a + ", off, 64);");
+                c.line(a + " = sanic_wave_sum(" + a + ");");
             }
         c.line("if (lane == 0) {");
         c.indent++;
@@ -1175,7 +1175,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
             if (SR > 0) {
                 c.line("float* red = u_lds + " + std::to_string(SC * K) + ";");
                 for (int i = 0; i < SR; i++) {
-                    c.line("for (int off = 32; off > 0; off >>= 1) racc" + std::to_string(i) + " += __shfl_xor(racc" + std::to_string(i) + ", off, 64);");
+                    c.line("racc" + std::to_string(i) + " = sanic_wave_sum(racc" + std::to_string(i) + ");");
                     c.line("if (lane == 0) red[wv * " + std::to_string(SR) + " + " + std::to_string(i) + "] = racc" + std::to_string(i) + ";");
                 }
             }
@@ -1327,7 +1327,7 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("}");
         for (int r = 0; r < SR; r++) {
             std::string rs = std::to_string(r);
-            k.line("for (int off = 32; off > 0; off >>= 1) rpart" + rs + " += __shfl_xor(rpart" + rs + ", off, 64);");
+            k.line("rpart" + rs + " = sanic_wave_sum(rpart" + rs + ");");
             k.line("if (lane == 0) rred[wv][" + rs + "] = rpart" + rs + ";");
         }
         k.line("__syncthreads();");
@@ -1349,7 +1349,7 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         for (int cs = 0; cs < SC; cs++)
             for (int j = 0; j < 8; j++) {
                 std::string a = "acc" + std::to_string(cs) + "_" + std::to_string(j);
-                k.line("for (int off = " + std::to_string(LPR) + "; off < 64; off <<= 1) " + a + " += __shfl_xor(" + a + ", off, 64);");
+                k.line(a + " = " + (LPR == 4 ? "sanic_stride4_sum(" : "sanic_stride8_sum(") + a + ");");
             }
         k.line("if (lane < " + std::to_string(LPR) + ") {");
         for (int cs = 0; cs < SC; cs++) {
