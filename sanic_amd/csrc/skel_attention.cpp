@@ -338,11 +338,14 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const int nvar = (int)(sizeof kVariants / sizeof *kVariants);
     const int var = st.sched.variant >= 0 && st.sched.variant < nvar ? st.sched.variant : 0;
     int NT = kVariants[var][0];
+    // long caches: 1024 threads × 256 positions keeps the chunk count near 16 (C3 at 4096
+    // positions: 8.9 µs against 9.6 µs for 512 × 128)
+    if (var == 0 && T >= 3072) NT = 1024;
     if (const char* e = getenv("SANIC_ATTN_NT")) NT = atoi(e) >= 1024 ? 1024 : atoi(e) >= 512 ? 512 : 256;
     const int NW = NT / 64;
     int CH = kVariants[var][1] ? kVariants[var][1] : NT / 4;
-    while (CH < 1024 && ((T + CH - 1) / CH) * REP * PSZ * 4 > 40 * 1024) CH *= 2;
     if (const char* e = getenv("SANIC_ATTN_CH")) CH = std::max(NT / 4, std::min(1024, atoi(e) / (NT / 4) * (NT / 4)));
+    while (CH < 1024 && ((T + CH - 1) / CH) * REP * PSZ * 4 > 40 * 1024) CH *= 2;
     const int64_t NCH = (T + CH - 1) / CH;
     const std::vector<RowWrite> writes = absorbed_writes(d, si, P);
     bool wk = false, wvv = false;
