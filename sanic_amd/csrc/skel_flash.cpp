@@ -24,6 +24,7 @@
 #include <cmath>
 
 #include <functional>
+#include <regex>
 
 #include "emit.h"
 #include "skeletons.h"
@@ -362,6 +363,13 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         << entry_full << sf.str() << "  return " << vfull << ";\n}\n";
     src << "__device__ __forceinline__ void window(const Args& a, idx_t hh, idx_t qrow, idx_t& lo, idx_t& hi) {\n"
         << Rw.entry() << wc.str() << "  lo = wlo; hi = whi;\n}\n";
+    // the same bounds before an empty window is widened to the whole stream; true = non-empty
+    {
+        static const std::regex reset(R"(\n *if \(whi <= wlo\) \{ wlo = 0; whi = \d+; \})");
+        const std::string raw = std::regex_replace(wc.str(), reset, "");
+        src << "__device__ __forceinline__ bool window_raw(const Args& a, idx_t hh, idx_t qrow, idx_t& lo, idx_t& hi) {\n"
+            << Rw.entry() << raw << "  lo = wlo; hi = whi;\n  return whi > wlo;\n}\n";
+    }
     src << "__device__ __forceinline__ void finish(const Args& a, const float* fs, idx_t hh, idx_t qi, idx_t ee) {\n"
         << Ro.entry() << fo.str() << "}\n";
 
@@ -403,6 +411,17 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("const idx_t khi = bhi_a > bhi_b ? bhi_a : bhi_b;");
     k.line("const idx_t wlo = wlo_a < wlo_b ? wlo_a : wlo_b, whi = whi_a > whi_b ? whi_a : whi_b;");
     k.line("const idx_t flo = wlo_a > wlo_b ? wlo_a : wlo_b, fhi = whi_a < whi_b ? whi_a : whi_b;");
+    // Edge tiles, per element: inside a row's honest window the score is the unmasked form
+    // (the full-tile identity); outside it −1e30 instead of the rendered mask (a finite mask
+    // gives that same value for any score below ~1e22; a −∞ mask differs only while a row has
+    // seen no visible key). Once a row has seen a visible key either weighs exactly 0, and what
+    // a row accumulated before that is scaled by α = exp(−1e30 − m) = 0 on its first visible
+    // tile, so the result is the same bit for bit — provided every row of the wave has a
+    // non-empty window (else the rendered leaf per element). A finite value, not −∞, keeps
+    // fully masked tiles at α = 1 (no rescale pass).
+    // (the row bounds are recomputed on edge tiles only: kept live across the loop they cost
+    // registers the window configuration spills)
+    const bool edge_on = !getenv("SANIC_FLASH_EDGE_OFF");
     // Q^T as the B operand (lane = query column l16 (+16·qt), d-slots lq·8 + 0..7 (+32·ds)),
     // read from LDS each tile rather than held in registers: the block's 128 query rows, 16-byte
     // chunks XOR-swizzled by row so the 16 rows a lane group reads hit different banks
@@ -546,11 +565,32 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         k.indent++;
     }
     // partial tiles (and scores of any other shape): the rendered leaf per element
-    k.line("#pragma unroll");
-    k.line("for (int kt = 0; kt < 4; ++kt)");
+    // (full and edge_fast are wave-uniform: one branch per tile, not a select per element)
+    k.line("int elo = -1, ehi = 0x7fffffff;");
+    if (edge_on) {
+        k.line("if (!full) {");
+        k.line("  idx_t rl, rh;");
+        k.line("  const bool ok = window_raw(a, hh, qi, rl, rh);");
+        k.line("  if (__all(ok)) { elo = (int)rl; ehi = (int)rh; } else { elo = 0x7fffffff; }");
+        k.line("}");
+    } else {
+        k.line("if (!full) elo = 0x7fffffff;");
+    }
+    k.line("if (elo != 0x7fffffff) {");
     k.line("  #pragma unroll");
-    k.line("  for (int r = 0; r < 4; ++r) sv[kt * 4 + r] = full ? score_full(a, s[kt][qt][r], (int)hh, qi, kb + kt * 16 + r)"
-           " : score_part(a, s[kt][qt][r], (int)hh, qi, kb + kt * 16 + r);");
+    k.line("  for (int kt = 0; kt < 4; ++kt)");
+    k.line("    #pragma unroll");
+    k.line("    for (int r = 0; r < 4; ++r) {");
+    k.line("      const int kj = kb + kt * 16 + r;");
+    k.line("      const float sf = score_full(a, s[kt][qt][r], (int)hh, qi, kj);");
+    k.line("      sv[kt * 4 + r] = kj >= elo && kj < ehi ? sf : -1e30f;");
+    k.line("    }");
+    k.line("} else {");
+    k.line("  #pragma unroll");
+    k.line("  for (int kt = 0; kt < 4; ++kt)");
+    k.line("    #pragma unroll");
+    k.line("    for (int r = 0; r < 4; ++r) sv[kt * 4 + r] = score_part(a, s[kt][qt][r], (int)hh, qi, kb + kt * 16 + r);");
+    k.line("}");
     k.line("float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));");
     k.line("#pragma unroll");
     k.line("for (int i = 4; i < 16; i += 2) mt = fmaxf(mt, fmaxf(sv[i], sv[i + 1]));");
