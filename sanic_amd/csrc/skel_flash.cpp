@@ -239,7 +239,6 @@ bool full_score_scale(const sanic_program_desc* d, int node, int dot, const std:
 }  // namespace
 
 bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
-    (void)scratch;
     FlashPlan P;
     if (!flash_plan(d, si, P)) return false;
     const sanic_stage& st = d->stages[si];
@@ -333,7 +332,15 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     src << "typedef short sanic_s16x4 __attribute__((ext_vector_type(4)));\n";
     src << "typedef short sanic_s16x8 __attribute__((ext_vector_type(8)));\n";
     src << "typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;\n";
-    src << R.args_struct({});
+    // tiling variants for the measured tuner: {3 workgroups per CU, 2 per CU, key range split
+    // in two}. The split form gives every (head, query block) two workgroups, each folding half
+    // of the block's key tiles; they exchange their (m, ℓ, o) partials through scratch and the
+    // second to arrive combines them (the carrier's ExpShifted combine with its −∞ guard) and
+    // projects. It evens out launches whose equal-sized blocks overfill the resident slots.
+    const int fvar = d->stages[si].sched.variant;
+    int SPL = fvar == 2 ? 2 : 1;
+    if (const char* e = getenv("SANIC_FLASH_SPLIT")) SPL = atoi(e) >= 2 ? 2 : 1;
+    src << (SPL > 1 ? R.args_struct({"float* __restrict__ scratch"}) : R.args_struct({}));
     src << "typedef __bf16 sanic_bf16x2 __attribute__((ext_vector_type(2)));\n";
     src << "typedef float sanic_f32x2 __attribute__((ext_vector_type(2)));\n";
     src << "__device__ __forceinline__ unsigned pk_bf16(float x, float y) {\n"
@@ -391,7 +398,13 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("const int l16 = lane & 15, lq = lane >> 4;");
     // XCD-aware block order: blockIdx mod 8 picks the KV head group, heaviest query blocks first
     const int64_t NKV = NH / P.rep;
-    k.line("const idx_t bid = blockIdx.x;");
+    const int64_t NB = NH * NQB;
+    if (SPL > 1) {
+        k.line("const idx_t bid = blockIdx.x % " + std::to_string(NB) + ";");   // partners share an XCD
+        k.line("const int part = (int)(blockIdx.x / " + std::to_string(NB) + ");");
+    } else {
+        k.line("const idx_t bid = blockIdx.x;");
+    }
     if (NKV % 8 == 0 || NKV == 8) {
         k.line("const idx_t kvh = bid % " + std::to_string(NKV) + ", rest = bid / " + std::to_string(NKV) + ";");
         k.line("const idx_t hh = kvh * " + std::to_string(P.rep) + " + rest % " + std::to_string(P.rep) + ";");
@@ -407,8 +420,16 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("window(a, hh, qb * 128 + 127, blo_b, bhi_b);");
     k.line("window(a, hh, q0, wlo_a, whi_a);");
     k.line("window(a, hh, q0 + 31, wlo_b, whi_b);");
-    k.line("const idx_t klo = (blo_a < blo_b ? blo_a : blo_b) / 64 * 64;");
-    k.line("const idx_t khi = bhi_a > bhi_b ? bhi_a : bhi_b;");
+    if (SPL > 1) {
+        k.line("const idx_t klo0 = (blo_a < blo_b ? blo_a : blo_b) / 64 * 64;");
+        k.line("const idx_t khi0 = bhi_a > bhi_b ? bhi_a : bhi_b;");
+        k.line("const idx_t ntl = khi0 > klo0 ? (khi0 - klo0 + 63) / 64 : 0;");
+        k.line("const idx_t klo = klo0 + (part * ntl / 2) * 64;");
+        k.line("const idx_t khi = part == 0 ? (klo0 + (ntl / 2) * 64 < khi0 ? klo0 + (ntl / 2) * 64 : khi0) : khi0;");
+    } else {
+        k.line("const idx_t klo = (blo_a < blo_b ? blo_a : blo_b) / 64 * 64;");
+        k.line("const idx_t khi = bhi_a > bhi_b ? bhi_a : bhi_b;");
+    }
     k.line("const idx_t wlo = wlo_a < wlo_b ? wlo_a : wlo_b, whi = whi_a > whi_b ? whi_a : whi_b;");
     k.line("const idx_t flo = wlo_a > wlo_b ? wlo_a : wlo_b, fhi = whi_a < whi_b ? whi_a : whi_b;");
     // Edge tiles, per element: inside a row's honest window the score is the unmasked form
@@ -670,6 +691,50 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("}");
     k.indent--;
     k.line("}");
+    int64_t soff = -1;
+    if (SPL > 1) {
+        // partials [block][part][36][256 lanes] (o in accumulator order, m, ℓ), then one arrival
+        // counter per block (zeroed at bind time, re-armed by the combining workgroup)
+        soff = scratch;
+        const int64_t pbytes = NB * 2 * 36 * 256 * 4;
+        scratch += pbytes + ((NB * 4 + 255) / 256) * 256;
+        k.line("{");
+        k.indent++;
+        k.line("float* pw = a.scratch + ((idx_t)bid * 2 + part) * 9216 + tid;");
+        k.line("#pragma unroll");
+        k.line("for (int dt = 0; dt < 4; ++dt)");
+        k.line("  #pragma unroll");
+        k.line("  for (int qt = 0; qt < 2; ++qt)");
+        k.line("    #pragma unroll");
+        k.line("    for (int r = 0; r < 4; ++r) sanic_st(pw + ((dt * 2 + qt) * 4 + r) * 256, o[dt][qt][r]);");
+        k.line("for (int qt = 0; qt < 2; ++qt) { sanic_st(pw + (32 + qt) * 256, m_run[qt]); sanic_st(pw + (34 + qt) * 256, lsum[qt][0]); }");
+        k.line("__builtin_amdgcn_s_waitcnt(0);");
+        k.line("__syncthreads();");
+        k.line("__shared__ int sp_last;");
+        k.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(pbytes) + ") + bid;");
+        k.line("if (tid == 0) sp_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;");
+        k.line("__syncthreads();");
+        k.line("if (!sp_last) return;");
+        k.line("if (tid == 0) sanic_st(cnt, 0u);");
+        // the combine is symmetric in its two operands (max, products, one sum), so the result
+        // does not depend on which half arrived last
+        k.line("const float* pr = a.scratch + ((idx_t)bid * 2 + (1 - part)) * 9216 + tid;");
+        k.line("#pragma unroll");
+        k.line("for (int qt = 0; qt < 2; ++qt) {");
+        k.line("  const float mo = sanic_ld(pr + (32 + qt) * 256), lo = sanic_ld(pr + (34 + qt) * 256);");
+        k.line("  const float M = __builtin_fmaxf(m_run[qt], mo);");
+        k.line("  const float ws = m_run[qt] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - M) * " + flit(LOG2E) + ");");
+        k.line("  const float wo = mo == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((mo - M) * " + flit(LOG2E) + ");");
+        k.line("  lsum[qt][0] = lsum[qt][0] * ws + lo * wo;");
+        k.line("  m_run[qt] = M;");
+        k.line("  #pragma unroll");
+        k.line("  for (int dt = 0; dt < 4; ++dt)");
+        k.line("    #pragma unroll");
+        k.line("    for (int r = 0; r < 4; ++r) o[dt][qt][r] = o[dt][qt][r] * ws + sanic_ld(pr + ((dt * 2 + qt) * 4 + r) * 256) * wo;");
+        k.line("}");
+        k.indent--;
+        k.line("}");
+    }
     // finish: the row sum across the 4 lane groups, then project per output point
     k.line("#pragma unroll");
     k.line("for (int qt = 0; qt < 2; ++qt) {");
@@ -696,10 +761,12 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     int occ = d->stages[si].sched.variant == 1 ? 2 : 3;
     if (const char* e = getenv("SANIC_FLASH_OCC")) occ = std::max(1, std::min(4, atoi(e)));
     src << "extern \"C\" __global__ void __launch_bounds__(256, " << occ << ") " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
-    out.kernel_kind = "skeleton:flash_prefill[rep " + std::to_string(P.rep) + "]";
+    out.kernel_kind = "skeleton:flash_prefill[rep " + std::to_string(P.rep) + "]" + (SPL > 1 ? "+split2" : "");
     out.source = src.str();
-    out.variants = 2;
-    out.launches.push_back({kname, "", dim3((unsigned)(NH * NQB)), dim3(256), 0, R.arg_list()});
+    out.variants = 3;
+    std::vector<Arg> args = R.arg_list();
+    if (SPL > 1) args.push_back({Arg::SCRATCH, soff});
+    out.launches.push_back({kname, "", dim3((unsigned)(NB * SPL)), dim3(256), 0, args});
     return true;
 }
 
