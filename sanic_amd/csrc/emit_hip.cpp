@@ -337,6 +337,23 @@ __device__ __forceinline__ float sanic_stride4_sum(float v) { // Î£ over lanes â
 __device__ __forceinline__ float sanic_stride8_sum(float v) { // Î£ over lanes â‰¡ i (mod 8)
   return sanic_rows_sum(v + sanic_dpp<0x128>(v));
 }
+// The partner's value at one step of an ascending butterfly (off = 1, 2, 4, ...): before the
+// step with offset `off` every aligned group of `off` lanes holds one value, so any lane of the
+// partner group serves â€” lane ^ 1 and lane ^ 2 by quad_perm, the other half of 8 by
+// row_half_mirror, the other half of 16 by row_mirror, then the permlane swaps.
+template <int OFF> __device__ __forceinline__ float sanic_bfly(float v) {
+  if constexpr (OFF == 1) return sanic_dpp<0xB1>(v, v);
+  else if constexpr (OFF == 2) return sanic_dpp<0x4E>(v, v);
+  else if constexpr (OFF == 4) return sanic_dpp<0x141>(v, v);
+  else if constexpr (OFF == 8) return sanic_dpp<0x140>(v, v);
+  else if constexpr (OFF == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+  } else {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+  }
+}
 __device__ __forceinline__ float sanic_lse(float a, float b) {
   if (a == -__builtin_huge_valf()) return b;
   if (b == -__builtin_huge_valf()) return a;
@@ -979,11 +996,13 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     body.line("}");
     // wave-level butterfly: the lower lane's partial is the left operand, so the merge order
     // follows lane order
-    body.line("for (int off = 1; off < 64; off <<= 1) {");
+    for (int off = 1; off < 64; off <<= 1) {
+    const std::string offs = std::to_string(off);
+    body.line("{");
     body.indent++;
     for (int k = 0; k < c.slots; k++)
-        body.line("float o" + std::to_string(k) + " = __shfl_xor(acc" + std::to_string(k) + ", off, 64);");
-    body.line("if (lane & off) {");
+        body.line("float o" + std::to_string(k) + " = sanic_bfly<" + offs + ">(acc" + std::to_string(k) + ");");
+    body.line("if (lane & " + offs + ") {");
     body.indent++;
     for (int k = 0; k < c.slots; k++)
         body.line("const float sw" + std::to_string(k) + " = acc" + std::to_string(k) + "; acc" + std::to_string(k) + " = o" +
@@ -993,6 +1012,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     emit_merge(R, body, c, "o");
     body.indent--;
     body.line("}");
+    }
     if (nw > 1) {
         body.line("__shared__ float lds_acc[" + std::to_string(nw) + "][" + std::to_string(c.slots) + "];");
         body.line("if (lane == 0) {");
@@ -1067,13 +1087,14 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
                       std::to_string(split) + " ? p : 0)) * " + std::to_string(c.slots) + ";");
             for (int k = 0; k < c.slots; k++)
                 body.line("float acc" + std::to_string(k) + " = live ? sanic_ld(pp + " + std::to_string(k) + ") : " + flit(c.identity[k]) + ";");
-            body.line("#pragma unroll");
-            body.line("for (int off = 1; off < " + std::to_string(LPP) + "; off <<= 1) {");
+            for (int off = 1; off < LPP; off <<= 1) {
+            const std::string offs = std::to_string(off);
+            body.line("{");
             body.indent++;
-            body.line("const bool up = (p & off) != 0;");
+            body.line("const bool up = (p & " + offs + ") != 0;");
             for (int k = 0; k < c.slots; k++) {
                 std::string ks = std::to_string(k);
-                body.line("const float o" + ks + " = __shfl_xor(acc" + ks + ", off, 64);");
+                body.line("const float o" + ks + " = sanic_bfly<" + offs + ">(acc" + ks + ");");
                 body.line("const float lo" + ks + " = up ? o" + ks + " : acc" + ks + ", hi" + ks + " = up ? acc" + ks + " : o" + ks + ";");
             }
             R.memo.emplace_back();
@@ -1085,6 +1106,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
             for (int k = 0; k < c.slots; k++) body.line("acc" + std::to_string(k) + " = nx" + std::to_string(k) + ";");
             body.indent--;
             body.line("}");
+            }
             body.line("if (p == 0 && gid < " + std::to_string(gvol) + ") {");
             body.indent++;
             R.memo.emplace_back();
