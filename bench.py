@@ -50,18 +50,20 @@ def device_weights(dev, shape, seed=1234):
 
 def dominant_kernel_roofline(dev, shape, weights, reps=40, copies=8):
     """The decode step's dominant kernel — the batched gate/up RMSNorm-fused GEMV with the
-    SwiGLU product computed per row pair (one launch: N = 2·ffn rows, K = hidden), on layer 0's
-    weights — `copies` launches per hipGraph replay, timed with HIP events on the library's
-    stream over `reps` back-to-back replays. Per-launch time = total / (reps · copies)."""
+    SwiGLU product computed per row pair (one launch: N = 2·ffn rows, K = hidden) — `copies`
+    launches per hipGraph replay, copy r on layer r's weights (8 × 67 MB overflows the 256 MB
+    Infinity Cache, so every launch streams cold weights from HBM as in the decode step), timed
+    with HIP events on the library's stream over `reps` back-to-back replays. Per-launch time =
+    total / (reps · copies)."""
     from sanic_amd import carrier as C
     from sanic_amd import ir
     from sanic_amd.program import STREAM, Program
     H, F = shape.hidden, shape.ffn
     p = Program()
     x = p.input("x", (H,), ir.F32)
-    g = p.input("g", (H,), ir.BF16)
-    ws = {nm: p.input(f"W{nm}", (F, H), ir.BF16) for nm in ("gate", "up")}
     for r in range(copies):
+        g = p.input(f"g{r}", (H,), ir.BF16)
+        ws = {nm: p.input(f"W{nm}{r}", (F, H), ir.BF16) for nm in ("gate", "up")}
         gu = {nm: p.fused(f"{nm}{r}", (F,), H, [(x, (STREAM,)), (g, (STREAM,)), (ws[nm], (0, STREAM))],
                           C.norm_fused_projection(H, shape.eps), ir.F32) for nm in ("gate", "up")}
         p.pointwise(f"h{r}", ir.map_(ir.MUL, ir.silu(gu["gate"]), gu["up"]), ir.F32)
@@ -69,9 +71,11 @@ def dominant_kernel_roofline(dev, shape, weights, reps=40, copies=8):
     kname = exe.stage_kernel(0)
     assert kname.startswith("skeleton:gemv[batched 2]+paired"), kname
     xb = dev.from_values([0.5] * H, ir.F32)
-    pre = "model.layers.0."
-    binds = {"x": xb, "g": weights[pre + "post_attention_layernorm.weight"],
-             "Wgate": weights[pre + "mlp.gate_proj.weight"], "Wup": weights[pre + "mlp.up_proj.weight"]}
+    binds = {"x": xb}
+    for r in range(copies):
+        pre = f"model.layers.{r % shape.layers}."
+        binds.update({f"g{r}": weights[pre + "post_attention_layernorm.weight"],
+                      f"Wgate{r}": weights[pre + "mlp.gate_proj.weight"], f"Wup{r}": weights[pre + "mlp.up_proj.weight"]})
     rp = exe.capture(binds)
     rp.step_many(5)
     secs = rp.step_many(reps) / (reps * copies)
