@@ -734,9 +734,10 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         const int64_t KQ = K / 4;
         const int KIq = (int)(KQ / 512);
         const int NSEG = (int)group.size();
-        // rows per workgroup: 4 for long rows and for very tall matrices (lm_head: fewer, fuller
-        // workgroups measured faster), else 2
-        int RBI = K >= 8192 || NTOT >= 65536 ? 4 : 2;
+        // rows per workgroup: 4 for very tall matrices (lm_head: fewer, fuller workgroups
+        // measured faster), else 2 (the measured tuner's pick for the 2048×8192 down
+        // projection in the decode step: 680 → 655 µs per step against 4)
+        int RBI = NTOT >= 65536 ? 4 : 2;
         // tiling variants for the measured tuner: rows per workgroup {rule, 1, 2, 4} ({2, 1}
         // for a paired launch, whose workgroup holds row i of every segment)
         const int gvar = d->stages[si].sched.variant;
