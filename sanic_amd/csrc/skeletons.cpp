@@ -738,11 +738,11 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         // measured faster), else 2 (the measured tuner's pick for the 2048×8192 down
         // projection in the decode step: 680 → 655 µs per step against 4)
         int RBI = NTOT >= 65536 ? 4 : 2;
-        // tiling variants for the measured tuner: rows per workgroup {rule, 1, 2, 4} ({2, 1}
+        // tiling variants for the measured tuner: rows per workgroup {rule, 1, 2, 4} ({2, 1, 4}
         // for a paired launch, whose workgroup holds row i of every segment)
         const int gvar = d->stages[si].sched.variant;
-        const int nvar = paired >= 0 ? 2 : 4;
-        if (gvar > 0 && gvar < nvar) RBI = paired >= 0 ? 1 : (1 << (gvar - 1));
+        const int nvar = paired >= 0 ? 3 : 4;
+        if (gvar > 0 && gvar < nvar) RBI = paired >= 0 ? (gvar == 1 ? 1 : 4) : (1 << (gvar - 1));
         if (const char* e = getenv("SANIC_GEMV_RB")) RBI = std::max(1, std::min(8, atoi(e)));
         if (paired >= 0 && !(gvar > 0 && gvar < nvar)) RBI = 2;
         if (paired >= 0) if (const char* e = getenv("SANIC_GEMV_PRB")) RBI = std::max(1, std::min(4, atoi(e)));
