@@ -334,7 +334,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     // one wave hide behind the other's), over 128-position chunks: measured in the full decode
     // step against 1024 threads × 256 positions (the measured tuner's pick, 3% per step)
     // tiling variants for the measured tuner: (threads, positions per chunk; 0 = the rule below)
-    static const int kVariants[][2] = {{512, 0}, {1024, 0}, {1024, 512}, {512, 256}, {256, 0}};
+    static const int kVariants[][2] = {{512, 0}, {1024, 0}, {1024, 512}, {512, 256}, {256, 0}, {256, 128}, {512, 512}};   // positions a multiple of NT/4
     const int nvar = (int)(sizeof kVariants / sizeof *kVariants);
     const int var = st.sched.variant >= 0 && st.sched.variant < nvar ? st.sched.variant : 0;
     int NT = kVariants[var][0];

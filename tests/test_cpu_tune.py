@@ -73,7 +73,7 @@ def test_decode_program_families():
     by_kernel = {}
     for f in fams:
         by_kernel.setdefault(f.kernel, []).append(f)
-    assert any(len(f.stages) == 16 and f.variants == 5 for f in by_kernel["sanic_attn_decode_h32_t2080"])
+    assert any(len(f.stages) == 16 and f.variants == 7 for f in by_kernel["sanic_attn_decode_h32_t2080"])
     assert any(len(f.stages) == 16 and f.variants == 3 for f in by_kernel["sanic_gemv_16384x2048"])
     assert any(len(f.stages) >= 15 and f.variants == 4 for f in by_kernel["sanic_gemv_2048x8192"])
     assert [len(f.stages) for f in by_kernel["sanic_gemv_128256x2048"]] == [1]
