@@ -371,9 +371,13 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     src << "__device__ __forceinline__ void window(const Args& a, idx_t hh, idx_t qrow, idx_t& lo, idx_t& hi) {\n"
         << Rw.entry() << wc.str() << "  lo = wlo; hi = whi;\n}\n";
     // the same bounds before an empty window is widened to the whole stream; true = non-empty
+    bool raw_ok = true;
     {
         static const std::regex reset(R"(\n *if \(whi <= wlo\) \{ wlo = 0; whi = \d+; \})");
         const std::string raw = std::regex_replace(wc.str(), reset, "");
+        // without the reset line removed, window_raw could not tell an empty window: edge
+        // tiles then take the rendered leaf
+        if (raw == wc.str() && wc.str().find("whi <= wlo") != std::string::npos) raw_ok = false;
         src << "__device__ __forceinline__ bool window_raw(const Args& a, idx_t hh, idx_t qrow, idx_t& lo, idx_t& hi) {\n"
             << Rw.entry() << raw << "  lo = wlo; hi = whi;\n  return whi > wlo;\n}\n";
     }
@@ -442,7 +446,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // fully masked tiles at α = 1 (no rescale pass).
     // (the row bounds are recomputed on edge tiles only: kept live across the loop they cost
     // registers the window configuration spills)
-    const bool edge_on = !getenv("SANIC_FLASH_EDGE_OFF");
+    const bool edge_on = raw_ok && !getenv("SANIC_FLASH_EDGE_OFF");
     // Q^T as the B operand (lane = query column l16 (+16·qt), d-slots lq·8 + 0..7 (+32·ds)),
     // read from LDS each tile rather than held in registers: the block's 128 query rows, 16-byte
     // chunks XOR-swizzled by row so the 16 rows a lane group reads hit different banks

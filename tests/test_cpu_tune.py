@@ -77,3 +77,16 @@ def test_decode_program_families():
     assert any(len(f.stages) == 16 and f.variants == 3 for f in by_kernel["sanic_gemv_16384x2048"])
     assert any(len(f.stages) >= 15 and f.variants == 4 for f in by_kernel["sanic_gemv_2048x8192"])
     assert [len(f.stages) for f in by_kernel["sanic_gemv_128256x2048"]] == [1]
+
+
+def test_flash_edge_tiles_use_the_raw_window():
+    """The flash skeleton's edge-tile path needs the row window before an empty window is
+    widened: the rendered window_raw has no reset line and the kernel calls it on edge tiles."""
+    import re
+    from sanic_amd import configs
+    for window in (0, 1024):
+        kind, src = configs.flash_prefill(window=window).emit(2)
+        assert kind.startswith("skeleton:flash_prefill")
+        raw = re.search(r"bool window_raw\(.*?\n\}", src, re.S).group(0)
+        assert "whi <= wlo" not in raw and "return whi > wlo;" in raw
+        assert "window_raw(a, hh, qi, rl, rh)" in src
