@@ -87,27 +87,65 @@ def dominant_kernel_roofline(dev, shape, weights, reps=40, copies=8):
             "us_per_launch": secs * 1e6}
 
 
-def cpu_baseline(shape, seconds_budget=20.0):
-    """The oracle's fused f64 decode step (oracle_llama_step) on this host at position 2048."""
-    import ctypes
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(shape, seconds_budget=24.0):
+    """The CPU path on this host, three legs, all outside the GPU's timed region:
+      - the oracle's fused f64 decode step (oracle_llama_step: the rustgen-shaped loops over the
+        bf16 weights) at positions 2048.. with every thread the host offers us (`value`),
+      - the same on one thread,
+      - the naive interpreter (oracle_run_program: interp.rs's node-by-node eval of the decode
+        schedule) on ONE layer of the model with the vocabulary cut to 16384, labelled as such
+        (the full model takes minutes per step this way).
+    The decode steps attend over a zero-filled 2048-position cache: the work per step equals a
+    real step's (every weight read once, attention over p + 1 positions); only the time is used."""
     import numpy as np
     import oracle
+    from sanic_amd import configs
     from tests.llama_ref import OracleModel, synth_weights
     threads = oracle.threads()
     w = synth_weights(shape, seed=99)
     om = OracleModel(shape, w)
-    n, t0 = 0, time.perf_counter()
-    tok = 1
-    while True:
-        tok, _ = om.step(tok, PROMPT + n)
-        n += 1
-        el = time.perf_counter() - t0
-        if el > seconds_budget / 4 or n >= 8:
-            break
+
+    def timed(nthreads, budget, max_steps):
+        n, t0, tok = 0, time.perf_counter(), 1
+        while True:
+            tok, _ = om.step(tok, PROMPT + n, nthreads)
+            n += 1
+            el = time.perf_counter() - t0
+            if el > budget or n >= max_steps:
+                return n, el
+
+    n, el = timed(threads, seconds_budget / 3, 8)
+    n1, el1 = timed(1, seconds_budget / 3, 4)
+    # the interpreter leg: one layer (same widths, vocabulary 16384), one step
+    one = configs.LlamaShape(layers=1, capacity=PROMPT + 1, vocab=16384)
+    prog = configs.llama_decode(one)
+    vals = {name: (w[name].reshape(-1)[:int(np.prod(shp))].astype(np.uint32) << 16).view(np.float32)
+            .astype(np.float64).reshape(shp) for name, shp in one.weight_shapes()}
+    vals["tokens"] = np.array([1.0])
+    vals["position"] = np.array(float(PROMPT))
+    t0 = time.perf_counter()
+    oracle.run_program(prog, vals)
+    el_i = time.perf_counter() - t0
+    del om, w, vals
     return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{n} decode steps of the full model at positions {PROMPT}..{PROMPT + n - 1} "
-                      f"(f64 fused loops over bf16 weights, {threads} threads, "
-                      f"{os.uname().nodename})"}
+                      f"(f64 fused loops over bf16 weights, {threads} threads)",
+            "single_thread_tok_s": n1 / el1, "single_thread_steps": n1,
+            "interpreter_one_layer_s_per_step": el_i,
+            "interpreter_sample": "one decode step of a 1-layer model (hidden 2048, ffn 8192, vocab 16384) "
+                                  "through the node-by-node interpreter, single thread",
+            "cpu_model": _cpu_model(), "host_cpus": os.cpu_count(), "host": os.uname().nodename}
 
 
 # ── secondary configurations (BASELINE.json configs B, C, D): one dominant kernel each ──
@@ -136,13 +174,14 @@ def _bind_random(dev, prog, keep, seed=7):
         if b.role not in (0, 1):
             continue
         n = int(__import__("math").prod(b.shape)) if b.shape else 1
+        base = b.name.split(".copy")[0]
         if b.dtype == ir.BF16:
             t = torch.randn(n, generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
-            if b.name in ("S", "Z"):
+            if base in ("S", "Z"):
                 t = (t.float().abs() * 0.005 + 0.001).to(torch.bfloat16)
         elif b.dtype == ir.F32:
             t = torch.zeros(max(n, 1), device="cuda", dtype=torch.float32)
-            if b.name == "position":
+            if base == "position":
                 t.fill_(4095.0)
         elif b.dtype in (ir.U4, ir.I4):
             t = torch.randint(0, 256, ((n + 1) // 2,), generator=g, device="cuda", dtype=torch.uint8)
@@ -162,74 +201,80 @@ def _time_program(dev, prog, keep, reps=20):
     return rp.step_many(reps) / reps, exe
 
 
-def bench_config(name: str, copies: int = 8):
+COLD_BYTES = 600 << 20      # more than twice the 256 MB Infinity Cache
+
+
+def config_row(dev, name: str):
+    """One secondary configuration's dominant kernel: `copies` launches per graph replay, each
+    on its own copy of the inputs (together more than twice the Infinity Cache), so every launch
+    reads cold inputs as it would in a real workload; plus the configuration's whole program
+    end to end (for C1/C2 with its RoPE stages). Per-launch times include the gap between
+    dependent launches inside the graph."""
     from sanic_amd import configs
-    from sanic_amd.backend import HipDevice
-    dev = HipDevice(0)
     keep = []
     if name in ("B1", "B1rows", "B2"):
         M = 512 if name == "B2" else 1
         mk = lambda: configs.rmsnorm_projection(M=M, kmajor=(name != "B1rows"))
-        main, K, N = 0, 2048, 8192
+        K, N = 2048, 8192
         flops = 2.0 * M * K * N + 2.0 * M * K
         nbytes = K * N * 2 + M * K * 2 + K * 2 + M * N * 2
         bound = "mfma" if name == "B2" else "hbm"
     elif name in ("D1", "D2"):
         M = 128 if name == "D2" else 1
         mk = lambda: configs.int4_matmul(M=M)
-        main, K, N = 0, 2048, 8192
+        K, N = 2048, 8192
         flops = 2.0 * M * K * N
         nbytes = N * K // 2 + 2 * (N * K // 64) * 2 + M * K * 2 + M * N * 2
         bound = "hbm" if name == "D1" else "both"
     elif name in ("C1", "C2"):
         w = 1024 if name == "C2" else 0
         mk = lambda: configs.flash_prefill(window=w, rope_stages=False)
-        main = 0
         S, NH, HD = 4096, 32, 64
-        if w:
-            pairs = w * (w + 1) / 2 + (S - w) * w
-        else:
-            pairs = S * (S + 1) / 2
+        pairs = (w * (w + 1) / 2 + (S - w) * w) if w else S * (S + 1) / 2
         flops = 4.0 * HD * NH * pairs
         nbytes = 2 * (NH * S * HD * 2) + 2 * (8 * S * HD * 2)
         bound = "mfma"
     elif name == "C3":
         mk = lambda: configs.decode_attention()
-        main = 0
         flops = 4.0 * 64 * 32 * 4096
         nbytes = 2 * 8 * 4096 * 64 * 2
         bound = "hbm"
     else:
         raise SystemExit(f"unknown config {name}; known: {sorted(CONFIGS)}")
-    # end-to-end: the configuration's whole program (for C1/C2 with the RoPE stages)
     full = configs.flash_prefill(window=(1024 if name == "C2" else 0)) if name in ("C1", "C2") else mk()
     t_full, exe_full = _time_program(dev, full, keep)
-    # the dominant kernel alone, `copies` launches per replay
     prog = mk()
-    prog.repeat_stage(main, copies - 1)
-    import os as _os
-    _os.environ["SANIC_HIP_NO_BATCH"] = "1"
-    t_k, exe = _time_program(dev, prog, keep)
-    del _os.environ["SANIC_HIP_NO_BATCH"]
+    in_bytes = sum(b.nbytes for b in prog.buffers if b.role == 0)
+    copies = max(8, min(128, -(-COLD_BYTES // max(in_bytes, 1))))
+    prog.repeat_stage(0, copies - 1, fresh_inputs=True)
+    os.environ["SANIC_HIP_NO_BATCH"] = "1"
+    try:
+        t_k, exe = _time_program(dev, prog, keep, reps=10)
+    finally:
+        del os.environ["SANIC_HIP_NO_BATCH"]
     per = t_k / copies
-    kind = exe.stage_kernel(main)
-    # the 8 launches share their inputs: those under 256 MB stay in the Infinity Cache
-    roof = {"bound": bound, "kernel": kind, "us_per_launch": per * 1e6, "traffic": None,
-            "inputs": "shared by the 8 timed launches (Infinity-Cache warm when under 256 MB)"}
+    row = {"kernel": exe.stage_kernel(0), "us_per_launch": per * 1e6, "bound": bound,
+           "launches_per_replay": copies, "inputs_per_launch_bytes": in_bytes,
+           "end_to_end_ms": t_full * 1e3, "flops": flops, "bytes": nbytes}
     if bound in ("hbm", "both"):
-        roof.update({"achieved": nbytes / per / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": nbytes / per / HBM_PEAK})
+        row.update({"achieved_GBps": nbytes / per / 1e9, "frac_hbm": nbytes / per / HBM_PEAK})
     if bound in ("mfma", "both"):
-        key = "achieved" if bound == "mfma" else "achieved_tflops"
-        roof.update({key: flops / per / 1e12})
-        if bound == "mfma":
-            roof.update({"peak": 2500.0, "unit": "TFLOP/s", "frac": flops / per / 2.5e15})
-        else:
-            roof.update({"frac_mfma": flops / per / 2.5e15})
-    out = {"metric": f"{name}: {CONFIGS[name]}", "value": (flops / t_full / 1e12) if bound == "mfma" else (nbytes / t_full / 1e9),
+        row.update({"achieved_TFLOPs": flops / per / 1e12, "frac_mfma": flops / per / 2.5e15})
+    row["frac"] = row["frac_mfma"] if bound == "mfma" else row["frac_hbm"]
+    del keep
+    return row, exe_full, full
+
+
+def bench_config(name: str):
+    from sanic_amd.backend import HipDevice
+    dev = HipDevice(0)
+    row, exe_full, full = config_row(dev, name)
+    bound = row["bound"]
+    t_full = row["end_to_end_ms"] * 1e-3
+    out = {"metric": f"{name}: {CONFIGS[name]}",
+           "value": (row["flops"] / t_full / 1e12) if bound == "mfma" else (row["bytes"] / t_full / 1e9),
            "unit": "TFLOP/s" if bound == "mfma" else "GB/s", "n_gpus": 1, "config": {"workload": CONFIGS[name]},
-           "ms_end_to_end": t_full * 1e3, "stages": [exe_full.stage_kernel(i) for i in range(len(full.stages))],
-           "roofline": roof, "flops": flops, "bytes": nbytes, "dtype": "bf16"}
+           "stages": [exe_full.stage_kernel(i) for i in range(len(full.stages))], "roofline": row, "dtype": "bf16"}
     print(json.dumps(out), flush=True)
 
 
@@ -282,6 +327,7 @@ def main():
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-configuration kernel rows")
     ap.add_argument("--pmc-probe", action="store_true", help="run only the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--tune", action="store_true",
                     help="run the measured tiling tuner (SANIC_TUNE) on the decode program first and "
@@ -361,6 +407,11 @@ def main():
     roof = dominant_kernel_roofline(dev, shape, weights)
     step_roof = {"bytes_per_step": step_bytes, "achieved_GBps": step_bytes / (ms * 1e-3) / 1e9,
                  "frac_of_8TBps": step_bytes / (ms * 1e-3) / HBM_PEAK}
+    rows = {}
+    if not args.no_configs:
+        for name in CONFIGS:
+            rows[name] = config_row(dev, name)[0]
+            log(f"{name}: {rows[name]['kernel']} {rows[name]['us_per_launch']:.2f} us/launch, frac {rows[name]['frac']:.3f}")
     cpu = None if args.no_cpu else cpu_baseline(shape)
     out = {
         "metric": "tok/s Llama-3.2-1B-shape bf16 decode", "value": tok_s, "unit": "tok/s",
@@ -370,7 +421,7 @@ def main():
         "config": {"workload": "llama3.2-1b-shape decode, 2048-token prompt prefilled token-by-token, "
                                f"greedy steps at positions {PROMPT}..{PROMPT + args.steps - 1}",
                    "global_batch": 1, "seq_len": PROMPT, "parallelism": "single-gpu"},
-        "roofline": roof, "step_roofline": step_roof, "cpu_baseline": cpu,
+        "roofline": roof, "step_roofline": step_roof, "cpu_baseline": cpu, "configs": rows,
         "gpu_event_seconds": gpu_s, "wall_seconds": wall,
         "prefill_token_by_token_tok_s": PROMPT / prefill_s,
     }

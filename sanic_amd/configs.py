@@ -243,18 +243,19 @@ def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
 
 def decode_attention(NH: int = 32, NKV: int = 8, HD: int = 64, cap: int = 4096,
                      theta: float = 500000.0, llama3_rope: bool = False, out_dtype: int = ir.BF16,
-                     sched: Sched = None) -> Program:
+                     sched: Sched = None, rope: bool = True) -> Program:
     """Config C (decode variant): one query token per head (RoPE at `position` applied in the
     score leaf) against a K cache [NKV, cap, HD] and a V cache stored transposed
     [NKV, HD, cap] (llama3_2.rs:160-173), GQA repeat-interleave, scale 1/√HD, prefix mask
-    `iota < position + 1` (−∞ beyond, llama3_2.rs:175-176)."""
+    `iota < position + 1` (−∞ beyond, llama3_2.rs:175-176). `rope=False` takes q as given
+    (already rotated), the form a prefill row is compared with."""
     p = Program()
     q = p.input("q", (NH, HD), ir.BF16)
     kc = p.input("k_cache", (NKV, cap, HD), ir.BF16)
     vc = p.input("v_cache", (NKV, HD, cap), ir.BF16)
     pos = p.input("position", (), ir.F32)
     invf = ir.llama3_inv_freq(theta, HD // 2) if llama3_rope else ir.rope_inv_freq(theta, HD // 2)
-    qr = ir.rope(ir.unsqueeze(q, 1), pos, invf)                              # [NH, 1, HD]
+    qr = ir.rope(ir.unsqueeze(q, 1), pos, invf) if rope else ir.unsqueeze(q, 1)   # [NH, 1, HD]
     rep = NH // NKV
     scores = ir.reduce(ir.map_(ir.MUL, qr, ir.expand_heads(kc, 0, rep)), 2, ir.M_ADD)
     scores = ir.map_(ir.MUL, scores, ir.const(1.0 / math.sqrt(HD)))

@@ -65,6 +65,10 @@ std::vector<WindowBound> honest_window(const sanic_program_desc* d, const sanic_
 void emit_window(Renderer& R, Code& code, const sanic_stage& st, const std::vector<WindowBound>& w,
                  const std::string& lo, const std::string& hi);
 int64_t dtype_bytes(int dt, int64_t n);
+// Last-arriver handshake: the workgroups sharing counter `cnt` each add 1 once their partials
+// are stored; `flag` (a __shared__ int it declares) is true in the one that arrives last.
+void emit_arrival(Code& k, const std::string& flag, const std::string& tid, const std::string& cnt,
+                  const std::string& expected);
 void validate(const sanic_program_desc* d);
 
 LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& scratch, const std::vector<int>& tails);

@@ -36,6 +36,22 @@ static int64_t vol(const int64_t* s, int r) {
 
 static std::vector<int64_t> shp(const sanic_node& n) { return {n.shape, n.shape + n.rank}; }
 
+// Ordering (HIP's scoped memory model): every thread's partial stores happen before the
+// barrier (workgroup scope), the barrier before thread 0's agent-scope release RMW, which
+// synchronises with the last arriver's acquire RMW on the same counter, which happens before
+// that workgroup's barrier and so before every one of its threads reads the partials. The
+// waitcnt makes each wave's own stores complete before the barrier, so the release has nothing
+// of theirs left in flight.
+void emit_arrival(Code& k, const std::string& flag, const std::string& tid, const std::string& cnt,
+                  const std::string& expected) {
+    k.line("__shared__ int " + flag + ";");
+    k.line("__builtin_amdgcn_s_waitcnt(0);");
+    k.line("__syncthreads();");
+    k.line("if (" + tid + " == 0) " + flag + " = __hip_atomic_fetch_add(" + cnt +
+           ", 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (" + expected + ") - 1u;");
+    k.line("__syncthreads();");
+}
+
 int64_t dtype_bytes(int dt, int64_t n) {
     switch (dt) {
     case SANIC_F64: return 8 * n;
@@ -1061,12 +1077,8 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     };
     if (fused_merge) {
         body.line("}");
-        body.line("__shared__ int sanic_last;");
         body.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(part_bytes) + ");");
-        body.line("__builtin_amdgcn_s_waitcnt(0);");
-        body.line("__syncthreads();");
-        body.line("if (t == 0) sanic_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;");
-        body.line("__syncthreads();");
+        emit_arrival(body, "sanic_last", "t", "cnt", "gridDim.x");
         body.line("if (!sanic_last) return;");
         // Few output points: L = split rounded up to a power of two lanes per point load one
         // partial each (all loads in flight at once) and merge in log2(L) butterfly steps of the
@@ -1075,7 +1087,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
         // point walks its partials.
         int LPP = 1;
         while (LPP < split) LPP <<= 1;
-        const bool butterfly = LPP <= 64 && gvol <= (int64_t)(nth / LPP) * 4 && !getenv("SANIC_FOLD_SERIAL_MERGE");
+        const bool butterfly = LPP <= 64 && gvol <= (int64_t)(nth / LPP) * 4;
         if (butterfly) {
             const int PPP = nth / LPP;                 // points per pass
             body.line("for (idx_t base = 0; base < " + std::to_string(gvol) + "; base += " + std::to_string(PPP) + ") {");

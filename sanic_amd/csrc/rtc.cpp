@@ -54,22 +54,13 @@ std::string compile_source(const std::string& generated) {
     for (auto* o : kOptions) opts_key += o, opts_key += ' ';
     char hex[32];
     snprintf(hex, sizeof hex, "%016llx", (unsigned long long)fnv1a(opts_key + generated));
-    // debugging: SANIC_HIP_DUMP=<dir> writes every generated source as <dir>/<hash>.hip;
-    // SANIC_HIP_OVERRIDE=<dir> compiles <dir>/<hash>.hip in place of the generated source
-    // when that file exists (a hand-edited variant of one kernel, e.g. with timestamps)
+    // debugging: SANIC_HIP_DUMP=<dir> writes every generated source as <dir>/<hash>.hip
     if (const char* dd = getenv("SANIC_HIP_DUMP")) {
         mkdir(dd, 0755);
         std::ofstream f(std::string(dd) + "/" + hex + ".hip");
         f << generated;
     }
-    std::string source = generated;
-    if (const char* od = getenv("SANIC_HIP_OVERRIDE")) {
-        std::string alt;
-        if (read_file(std::string(od) + "/" + hex + ".hip", alt)) {
-            source = alt;
-            snprintf(hex, sizeof hex, "%016llx", (unsigned long long)fnv1a(opts_key + source));
-        }
-    }
+    const std::string& source = generated;
     std::string dir = cache_dir();
     std::string path = dir + "/" + hex + ".co";
     std::string code;

@@ -274,7 +274,7 @@ bool row_mapping_ok(const Sym& addr, int REP, int64_t NG, int64_t T, int64_t X, 
 
 std::vector<RowWrite> absorbed_writes(const sanic_program_desc* d, int ai, const AttnPlan& P) {
     std::vector<RowWrite> out;
-    if (getenv("SANIC_HIP_NO_ABSORB") || getenv("SANIC_HIP_GENERIC")) return out;
+    if (getenv("SANIC_HIP_GENERIC")) return out;
     const int64_t NG = P.NH / P.rep;
     for (int s = ai - 1; s >= 0 && out.size() < 2; s--) {
         const sanic_stage& st = d->stages[s];
@@ -341,10 +341,8 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     // long caches: 1024 threads × 256 positions keeps the chunk count near 16 (C3 at 4096
     // positions: 8.9 µs against 9.6 µs for 512 × 128)
     if (var == 0 && T >= 3072) NT = 1024;
-    if (const char* e = getenv("SANIC_ATTN_NT")) NT = atoi(e) >= 1024 ? 1024 : atoi(e) >= 512 ? 512 : 256;
     const int NW = NT / 64;
     int CH = kVariants[var][1] ? kVariants[var][1] : NT / 4;
-    if (const char* e = getenv("SANIC_ATTN_CH")) CH = std::max(NT / 4, std::min(1024, atoi(e) / (NT / 4) * (NT / 4)));
     while (CH < 1024 && ((T + CH - 1) / CH) * REP * PSZ * 4 > 40 * 1024) CH *= 2;
     const int64_t NCH = (T + CH - 1) / CH;
     const std::vector<RowWrite> writes = absorbed_writes(d, si, P);
@@ -356,7 +354,7 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     // contributes that single position as its own partial carrier (m = its score, ℓ = 1, o = its
     // value row); the regular chunks leave the position out. No regular chunk then waits on the
     // row's loads and RoPE arithmetic, which otherwise put the chunk holding the row last.
-    bool sep = wk && wvv && !getenv("SANIC_ATTN_INCHUNK_WRITE");
+    bool sep = wk && wvv;
     if (sep) {
         std::string rp[2];
         for (int i = 0; i < 2; i++) {
@@ -793,12 +791,8 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     if (GP * 4 > 64 * 1024) return false;
     k.line("{");
     k.indent++;
-    k.line("__shared__ int sanic_last;");
-    k.line("__builtin_amdgcn_s_waitcnt(0);");
-    k.line("__syncthreads();");
     k.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(counter_off) + ") + grp;");
-    k.line("if (tid == 0) sanic_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == " + std::to_string(NPART) + "u - 1u;");
-    k.line("__syncthreads();");
+    emit_arrival(k, "sanic_last", "tid", "cnt", std::to_string(NPART) + "u");
     k.line("if (!sanic_last) return;");
     k.line("__shared__ __attribute__((aligned(16))) float g_lds[" + std::to_string(GP) + "];");
     k.line("__shared__ float w_lds[" + std::to_string(REP) + "][" + std::to_string(NPART) + "];");

@@ -339,7 +339,6 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // projects. It evens out launches whose equal-sized blocks overfill the resident slots.
     const int fvar = d->stages[si].sched.variant;
     int SPL = fvar == 2 ? 2 : 1;
-    if (const char* e = getenv("SANIC_FLASH_SPLIT")) SPL = atoi(e) >= 2 ? 2 : 1;
     src << (SPL > 1 ? R.args_struct({"float* __restrict__ scratch"}) : R.args_struct({}));
     src << "typedef __bf16 sanic_bf16x2 __attribute__((ext_vector_type(2)));\n";
     src << "typedef float sanic_f32x2 __attribute__((ext_vector_type(2)));\n";
@@ -387,15 +386,12 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     const std::string kname = "sanic_flash_h" + std::to_string(NH) + "_s" + std::to_string(NQ) + "_t" + std::to_string(T);
     Code k;
     k.indent = 1;
-    int KS = 72;      // LDS row stride (bf16) of the K tile: 64 + 8 padding
-    int VS = 72;      // LDS row stride of the V tile
-    if (const char* e = getenv("SANIC_FLASH_KS")) KS = std::max(64, atoi(e) / 8 * 8);
-    if (const char* e = getenv("SANIC_FLASH_VS")) VS = std::max(64, atoi(e) / 8 * 8);
+    const int VS = 72;   // LDS row stride (bf16) of the V tile: 64 + 8 padding
     // K rows: unpadded 128-byte rows with the 16-byte chunk index XORed by (row mod 8), like
     // the Q tile — a 72-element padded stride puts the 16 rows of one fragment read into 2-way
     // bank conflicts on gfx950 (measured: twice the LDS cycles of the swizzled form)
-    const bool kswz = !getenv("SANIC_FLASH_KPAD") && !getenv("SANIC_FLASH_KS");
-    if (kswz) KS = 64;
+    const bool kswz = true;
+    const int KS = 64;
     k.line("__shared__ unsigned short k_lds[2][64 * " + std::to_string(KS) + "];");
     k.line("__shared__ unsigned short v_lds[2][64 * " + std::to_string(VS) + "];");
     k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
@@ -446,7 +442,9 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // fully masked tiles at α = 1 (no rescale pass).
     // (the row bounds are recomputed on edge tiles only: kept live across the loop they cost
     // registers the window configuration spills)
-    const bool edge_on = raw_ok && !getenv("SANIC_FLASH_EDGE_OFF");
+    // (variant 3 takes the rendered leaf on every edge tile: the reference form the fast path
+    // is tested against bit for bit)
+    const bool edge_on = raw_ok && fvar != 3;
     // Q^T as the B operand (lane = query column l16 (+16·qt), d-slots lq·8 + 0..7 (+32·ds)),
     // read from LDS each tile rather than held in registers: the block's 128 query rows, 16-byte
     // chunks XOR-swizzled by row so the 16 rows a lane group reads hit different banks
@@ -476,7 +474,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         for (int ch : {x.a, x.b, x.c}) if (ch >= 0 && reads_f(ch)) return true;
         return false;
     };
-    const bool lazy = !reads_f(c.project) && !getenv("SANIC_FLASH_EAGER");
+    const bool lazy = !reads_f(c.project);
     const double TAU = 8.0 / LOG2E;
     // cooperative tile loads: K tile (64 keys × 64 d) and V tile, 2 × 16 B per thread each
     std::string kbase = std::to_string(P.kacc.addr.c0) + " + " + hterm(kc, kh, khc);
@@ -712,16 +710,13 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         k.line("    #pragma unroll");
         k.line("    for (int r = 0; r < 4; ++r) sanic_st(pw + ((dt * 2 + qt) * 4 + r) * 256, o[dt][qt][r]);");
         k.line("for (int qt = 0; qt < 2; ++qt) { sanic_st(pw + (32 + qt) * 256, m_run[qt]); sanic_st(pw + (34 + qt) * 256, lsum[qt][0]); }");
-        k.line("__builtin_amdgcn_s_waitcnt(0);");
-        k.line("__syncthreads();");
-        k.line("__shared__ int sp_last;");
         k.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(pbytes) + ") + bid;");
-        k.line("if (tid == 0) sp_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;");
-        k.line("__syncthreads();");
+        emit_arrival(k, "sp_last", "tid", "cnt", "2u");
         k.line("if (!sp_last) return;");
         k.line("if (tid == 0) sanic_st(cnt, 0u);");
-        // the combine is symmetric in its two operands (max, products, one sum), so the result
-        // does not depend on which half arrived last
+        // the combine always takes part 0's values as the left operand of one explicit fma
+        // (a·wa + b·wb with the product b·wb rounded first), so the rounding does not depend on
+        // which half arrived last
         k.line("const float* pr = a.scratch + ((idx_t)bid * 2 + (1 - part)) * 9216 + tid;");
         k.line("#pragma unroll");
         k.line("for (int qt = 0; qt < 2; ++qt) {");
@@ -729,12 +724,16 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         k.line("  const float M = __builtin_fmaxf(m_run[qt], mo);");
         k.line("  const float ws = m_run[qt] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - M) * " + flit(LOG2E) + ");");
         k.line("  const float wo = mo == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((mo - M) * " + flit(LOG2E) + ");");
-        k.line("  lsum[qt][0] = lsum[qt][0] * ws + lo * wo;");
+        k.line("  const bool p0 = part == 0;");
+        k.line("  lsum[qt][0] = p0 ? __builtin_fmaf(lsum[qt][0], ws, lo * wo) : __builtin_fmaf(lo, wo, lsum[qt][0] * ws);");
         k.line("  m_run[qt] = M;");
         k.line("  #pragma unroll");
         k.line("  for (int dt = 0; dt < 4; ++dt)");
         k.line("    #pragma unroll");
-        k.line("    for (int r = 0; r < 4; ++r) o[dt][qt][r] = o[dt][qt][r] * ws + sanic_ld(pr + ((dt * 2 + qt) * 4 + r) * 256) * wo;");
+        k.line("    for (int r = 0; r < 4; ++r) {");
+        k.line("      const float ov = sanic_ld(pr + ((dt * 2 + qt) * 4 + r) * 256);");
+        k.line("      o[dt][qt][r] = p0 ? __builtin_fmaf(o[dt][qt][r], ws, ov * wo) : __builtin_fmaf(ov, wo, o[dt][qt][r] * ws);");
+        k.line("    }");
         k.line("}");
         k.indent--;
         k.line("}");
@@ -763,11 +762,10 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // register cap costs a few spilled values outside the inner loop)
     // tiling variants for the measured tuner: workgroups per CU {3, 2}
     int occ = d->stages[si].sched.variant == 1 ? 2 : 3;
-    if (const char* e = getenv("SANIC_FLASH_OCC")) occ = std::max(1, std::min(4, atoi(e)));
     src << "extern \"C\" __global__ void __launch_bounds__(256, " << occ << ") " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     out.kernel_kind = "skeleton:flash_prefill[rep " + std::to_string(P.rep) + "]" + (SPL > 1 ? "+split2" : "");
     out.source = src.str();
-    out.variants = 3;
+    out.variants = 4;
     std::vector<Arg> args = R.arg_list();
     if (SPL > 1) args.push_back({Arg::SCRATCH, soff});
     out.launches.push_back({kname, "", dim3((unsigned)(NB * SPL)), dim3(256), 0, args});

@@ -168,21 +168,18 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     const sanic_carrier& c = st.carrier;
     const int64_t M = P.M, N = P.N, K = P.K;
     int BM = M % 128 == 0 ? 128 : 64;
-    if (const char* e = getenv("SANIC_GEMM_BM")) BM = atoi(e) <= 64 && M % 64 == 0 ? 64 : BM;
     int BN = 128;
     while (BN > 32 && (M / BM) * (N / BN) < 256) BN /= 2;
-    if (const char* e = getenv("SANIC_GEMM_BN")) BN = std::max(32, std::min(128, atoi(e)));
     if (N % BN) return false;
     const int WM = BM / 2, WN = BN / 2;       // per-wave tile
     const int MT = WM / 16, NT = WN / 16;
     const int SR = (int)P.rslots.size();
     int AS = 64 + 8;                          // LDS row strides (bf16)
     int BS = 64 + 8;
-    if (const char* e = getenv("SANIC_GEMM_AS")) AS = std::max(64, atoi(e) / 8 * 8);
     // k-contiguous tiles: unpadded 128-byte rows with the 16-byte chunk index XORed by
     // (row mod 8) — a 72-element padded stride 2-way bank-conflicts the 16-row operand reads
     // on gfx950
-    const bool kswz = !getenv("SANIC_GEMM_APAD") && !getenv("SANIC_GEMM_AS");
+    const bool kswz = true;
     if (kswz) AS = BS = 64;
     // element offset of (row, k) in a k-contiguous tile; k a multiple of 8
     auto koff = [&](const std::string& row, const std::string& k8, int stride) {
@@ -234,7 +231,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         cwt[j] = b == SANIC_BIND_STREAM ? Sym::var(0) : b == P.ndim ? Sym::var(1) : Sym();
     }
     bool bkn = false;
-    if (!contig && !getenv("SANIC_GEMM_NO_TR")) {
+    if (!contig) {
         std::vector<int> tb, td;
         bool tok = true, tc = true;
         std::string tr;
@@ -242,8 +239,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         render_weight_run(d, st.leaf[P.w], cwt, {K, N}, l1, d1, "kk", "n0", "_p", tb, td, tok, tc, tr, false);
         bkn = tok && tc;
     }
-    int BNS = BN + 8;                         // [k][n] B tile row stride (bf16)
-    if (const char* e = getenv("SANIC_GEMM_BPAD")) BNS = BN + std::max(0, atoi(e) / 4 * 4);
+    const int BNS = BN + 8;                   // [k][n] B tile row stride (bf16)
     // row leaves vector forms over vars {0: m, 1: k}
     std::vector<std::vector<Sym>> crow;
     for (int l : P.rows) {
@@ -265,7 +261,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     // A operands that need arithmetic (x·g of the fused RMSNorm) are built once by a first
     // launch into bf16 hi/lo planes [M][K] (plus the row slots), instead of by every one of the
     // N/BN column workgroups
-    const bool pre = splitA && N / BN >= 4 && K % 512 == 0 && !getenv("SANIC_GEMM_NO_PRE");
+    const bool pre = splitA && N / BN >= 4 && K % 512 == 0;
     int64_t hi_off = 0, lo_off = 0, rs_off = 0;
     Code kp;
     kp.indent = 1;
@@ -545,7 +541,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     // so a tile's global loads (≈2 µs under load) must be in flight for two tiles' MFMAs, not
     // one. Two register sets alternate in a loop unrolled by two; a set's loaded values are
     // plain variables declared before the loop (the loads' address temporaries stay scoped).
-    const bool deep = NKT % 2 == 0 && NKT >= 4 && !getenv("SANIC_GEMM_SHALLOW");
+    const bool deep = NKT % 2 == 0 && NKT >= 4;
     if (deep) {
         auto persistent = [&](const std::string& sfx, Code& decl) {
             Code tmp;

@@ -596,11 +596,7 @@ void emit_tail(Renderer& R, Code& k, const sanic_program_desc* d, const std::vec
     for (int t : tails) R.coherent.insert(d->stages[t].out_buffer);
     k.line("{");
     k.indent++;
-    k.line("__shared__ int sanic_last;");
-    k.line("__builtin_amdgcn_s_waitcnt(0);");
-    k.line("__syncthreads();");
-    k.line("if (threadIdx.x == 0) sanic_last = __hip_atomic_fetch_add(" + counter + ", 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (" + expected + ") - 1;");
-    k.line("__syncthreads();");
+    emit_arrival(k, "sanic_last", "threadIdx.x", counter, expected);
     k.line("if (sanic_last) {");
     k.indent++;
     for (size_t i = 0; i < tails.size(); i++) {
@@ -691,7 +687,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
     {
         bool same = group.size() >= 2;
         for (auto& P : group) same = same && P.N == P0.N;
-        if (same && !getenv("SANIC_HIP_NO_PAIR") && paired_candidate(d, si + (int)group.size(), P0.N)) paired = si + (int)group.size();
+        if (same && paired_candidate(d, si + (int)group.size(), P0.N)) paired = si + (int)group.size();
         if (paired >= 0) {
             // it may read only group outputs and buffers nobody in the group writes
             std::set<int> reads;
@@ -714,11 +710,9 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
     for (auto& P : group) { seg_off.push_back(NTOT); NTOT += P.N; }
     const int KI = (int)((K + 511) / 512);
     int RQ = K <= 2048 ? 2 : 1;                  // rows in flight per wave iteration
-    if (const char* e = getenv("SANIC_GEMV_RQ")) RQ = std::max(1, std::min(4, atoi(e)));
     if (paired >= 0) RQ = (int)group.size();     // row i of every segment in one wave
     int64_t waves = (NTOT + RQ - 1) / RQ;
-    int64_t max_blocks = 1024;
-    if (const char* e = getenv("SANIC_GEMV_BLOCKS")) max_blocks = std::max(1, atoi(e));
+    const int64_t max_blocks = 1024;
     int64_t blocks = std::min<int64_t>((waves + 3) / 4, max_blocks);
     int64_t counter_off = -1;
     if (!tails.empty()) {
@@ -730,7 +724,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
     // its activation factors in registers (loaded once, reused by all rows of the workgroup),
     // and the per-wave partials meet in LDS once at the end: no LDS staging of the activation
     // and no barrier before the weight FMAs.
-    if (K % 2048 == 0 && K <= 16384 && !getenv("SANIC_GEMV_V1")) {
+    if (K % 2048 == 0 && K <= 16384) {
         const int64_t KQ = K / 4;
         const int KIq = (int)(KQ / 512);
         const int NSEG = (int)group.size();
@@ -743,9 +737,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         const int gvar = d->stages[si].sched.variant;
         const int nvar = paired >= 0 ? 3 : 4;
         if (gvar > 0 && gvar < nvar) RBI = paired >= 0 ? (gvar == 1 ? 1 : 4) : (1 << (gvar - 1));
-        if (const char* e = getenv("SANIC_GEMV_RB")) RBI = std::max(1, std::min(8, atoi(e)));
         if (paired >= 0 && !(gvar > 0 && gvar < nvar)) RBI = 2;
-        if (paired >= 0) if (const char* e = getenv("SANIC_GEMV_PRB")) RBI = std::max(1, std::min(4, atoi(e)));
         const int RB = paired >= 0 ? RBI * NSEG : RBI;           // rows per workgroup
         const int64_t UNITS = paired >= 0 ? P0.N : NTOT;
         const int64_t nblocks = (UNITS + RBI - 1) / RBI;
@@ -834,7 +826,7 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         }
         // epilogue operands of each row, requested behind the weights (single-segment launches)
         std::vector<std::map<int, std::string>> epi_pre(RB);
-        if (group.size() == 1 && paired < 0 && st0.epilogue >= 0 && !getenv("SANIC_GEMV_NO_EPI_PREFETCH"))
+        if (group.size() == 1 && paired < 0 && st0.epilogue >= 0)
             for (int q = 0; q < RB; q++) {
                 std::vector<std::string> gc(st0.rank, "0");
                 gc[P0.ndim] = "nn" + std::to_string(q);
@@ -1271,12 +1263,10 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     // a quarter of K each; lanes of one column group meet by shuffles, waves in LDS. Strips are
     // dealt XCD-aware: workgroups b and b + 8 (one XCD) own adjacent strips, so the two halves of
     // a 128-byte line are read through the same L2.
-    int SW = 32;                                  // strip width (columns); 64 measured slower
-    if (const char* e = getenv("SANIC_GEMVT_SW")) SW = atoi(e) <= 32 ? 32 : 64;
-    int NT = 512;                                 // 8 waves: 16 (SW 32) / 32 (SW 64) row loads per lane
-    if (const char* e = getenv("SANIC_GEMVT_NT")) NT = atoi(e) >= 1024 ? 1024 : atoi(e) >= 512 ? 512 : 256;
+    const int SW = 32;                            // strip width (columns); 64 measured slower
+    const int NT = 512;                           // 8 waves: 16 row loads per lane
     const int LPR = SW / 8, RPS = 64 / LPR, NWV = NT / 64;   // lanes per row, rows per step, waves
-    if (N % (SW * 8) == 0 && K % (RPS * NWV) == 0 && K <= 8192 && !getenv("SANIC_GEMVT_SLICES")) {
+    if (N % (SW * 8) == 0 && K % (RPS * NWV) == 0 && K <= 8192) {
         const int SC = (int)P.cslots.size(), SR = (int)P.rslots.size();
         const int64_t NS = N / SW, KQ = K / NWV, IT = KQ / RPS;   // strips, rows per wave, row steps
         Renderer R(d);
@@ -1395,7 +1385,6 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const int SC = (int)P.cslots.size(), SR = (int)P.rslots.size();
     const int64_t NCG = N / 512;
     int64_t KS = std::max<int64_t>(1, std::min<int64_t>(K / 128, 128 / NCG));   // K slices
-    if (const char* e = getenv("SANIC_GEMVT_KS")) KS = std::max<int64_t>(1, atoi(e));
     while (K % KS || (K / KS) % 4) KS--;
     const int64_t KB = K / KS, KW = KB / 4;                                    // rows per slice / wave
     int64_t part_off = scratch;
@@ -1489,12 +1478,8 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     k.line("  const int cs = i / 512, col = i % 512;");
     k.line("  sanic_st(a.scratch + " + std::to_string(part_off / 4) + " + (ks * " + std::to_string(SC) + " + cs) * " + std::to_string(N) + " + cg * 512 + col, v);");
     k.line("}");
-    k.line("__shared__ int sanic_last;");
-    k.line("__builtin_amdgcn_s_waitcnt(0);");
-    k.line("__syncthreads();");
     k.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(counter_off) + ") + cg;");
-    k.line("if (t == 0) sanic_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == " + std::to_string(KS) + "u - 1u;");
-    k.line("__syncthreads();");
+    emit_arrival(k, "sanic_last", "t", "cnt", std::to_string(KS) + "u");
     k.line("if (!sanic_last) return;");
     k.line("if (t == 0) sanic_st(cnt, 0u);");
     // row slots: the K slices' partials, in slice order

@@ -121,9 +121,11 @@ class Program:
         self.stages.append(Stage(1, name, out, grid, value=value, where=where))
         return self.node(out.name)
 
-    def repeat_stage(self, i: int, copies: int) -> List[str]:
+    def repeat_stage(self, i: int, copies: int, fresh_inputs: bool = False) -> List[str]:
         """Append `copies` more instances of stage `i`, each writing its own output buffer
-        (for timing one kernel as back-to-back launches inside one captured graph)."""
+        (for timing one kernel as back-to-back launches inside one captured graph). With
+        `fresh_inputs` every copy reads its own copies of the stage's INPUT buffers
+        (`<name>.copy<r>`), so back-to-back launches do not find each other's inputs in cache."""
         import copy as _copy
         st = self.stages[i]
         names = []
@@ -133,6 +135,32 @@ class Program:
             dup = _copy.copy(st)
             dup.out = out
             dup.name = name
+            if fresh_inputs:
+                memo: Dict[int, ir.Node] = {}
+
+                def ren(n: ir.Node) -> ir.Node:
+                    if id(n) in memo:
+                        return memo[id(n)]
+                    if n.kind == ir.INPUT and self.by_name[n.name].role == INPUT:
+                        cn = f"{n.name}.copy{r}"
+                        if cn not in self.by_name:
+                            b = self.by_name[n.name]
+                            self._decl(cn, INPUT, b.shape, b.dtype)
+                        m = _copy.copy(n)
+                        m.name = cn
+                    elif n.inputs:
+                        m = _copy.copy(n)
+                        m.inputs = tuple(ren(c) for c in n.inputs)
+                    else:
+                        m = n
+                    memo[id(n)] = m
+                    return m
+                if st.kind == 0:
+                    dup.leaves = [(ren(nd), b) for nd, b in st.leaves]
+                    dup.epilogue = ren(st.epilogue) if st.epilogue is not None else None
+                else:
+                    dup.value = ren(st.value)
+                    dup.where = ren(st.where) if st.where is not None else None
             self.stages.append(dup)
             names.append(name)
         return names

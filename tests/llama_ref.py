@@ -68,10 +68,10 @@ class OracleModel:
             self.kc[l][...] = kc[l]
             self.vc[l][...] = vc[l]
 
-    def step(self, token: int, pos: int):
+    def step(self, token: int, pos: int, nthreads: int = 0):
         logits = np.empty(self.shape.vocab, np.float64)
         tok = oracle.lib().oracle_llama_step(ctypes.byref(self.m), token, pos, logits.ctypes.data,
-                                             oracle.threads())
+                                             nthreads or oracle.threads())
         return int(tok), logits
 
 
