@@ -220,6 +220,16 @@ class Executable:
                 res[b.name] = Buffer(self.dev, outs[b.index], b.nbytes)
         return res
 
+    def execute_static(self, bindings: Dict[str, Buffer]):
+        """sanic_hip_execute_static: run once with no device allocation — `bindings` holds the
+        caller's buffers for every INPUT, STATE and OUTPUT buffer; intermediates and the
+        split/counter arena use the library's static scratch. Returns without waiting."""
+        missing = [b.name for b in self.prog.buffers if b.role == OUTPUT and b.name not in bindings]
+        if missing:
+            raise KeyError(f"outputs must be bound: {missing}")
+        arr = self._bindings(bindings)
+        abi.check(abi.lib().sanic_hip_execute_static(self.handle, arr, len(self.prog.buffers)))
+
     def capture(self, bindings: Dict[str, Buffer], feedback: Sequence = ()) -> "Replay":
         """Program::capture: freeze the bindings into one hipGraph; `feedback` pairs
         (output name, input name) copy an output into an input at the end of each step."""

@@ -30,7 +30,18 @@ struct sanic_hip_device {
     int ordinal = 0;
     hipStream_t stream = nullptr;
     hipDeviceProp_t props{};
+    char* scratch_ptr = nullptr;   // this GPU's copy of `scratch` (execute_static)
 };
+
+// ── the static scratch of sanic_hip_execute_static ─────────────────────────────────────────
+// Device memory that entry point uses beyond the caller's inputs and outputs: the
+// executable's split-partial / arrival-counter arena and its intermediate (SCRATCH-role)
+// buffers, laid out back to back at 256-byte alignment. Every GPU the library runs on holds
+// its own copy until the process ends. In host code `scratch` names a host-side stand-in, not
+// a device address: host code uses only the per-device address hipGetSymbolAddress returns
+// (sanic_hip_device::scratch_ptr, taken in sanic_hip_open with the device current).
+static const size_t kStaticScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) char scratch[kStaticScratchBytes];
 
 struct Storage {
     void* ptr = nullptr;
@@ -198,7 +209,7 @@ static void compile_all(sanic_hip_exe* exe, bool load) {
 }
 
 // Enqueue every stage's launches on the device stream. `bound[i]` is program buffer i.
-static void enqueue(sanic_hip_exe* exe, const std::vector<sanic_hip_buffer*>& bound, char* scratch,
+static void enqueue(sanic_hip_exe* exe, const std::vector<sanic_hip_buffer*>& bound, char* arena,
                     hipEvent_t* stage_events = nullptr) {
     hipStream_t s = exe->dev->stream;
     for (size_t si = 0; si < exe->low.stages.size(); si++) {
@@ -207,7 +218,7 @@ static void enqueue(sanic_hip_exe* exe, const std::vector<sanic_hip_buffer*>& bo
             if (l.zero_scratch && l.zero_bytes > 0) {
                 int64_t words = l.zero_bytes / 4;
                 unsigned blocks = (unsigned)std::min<int64_t>((words + 255) / 256, 4096);
-                hipLaunchKernelGGL(sanic_zero_words, dim3(blocks), dim3(256), 0, s, (uint32_t*)(scratch + l.zero_off), words);
+                hipLaunchKernelGGL(sanic_zero_words, dim3(blocks), dim3(256), 0, s, (uint32_t*)(arena + l.zero_off), words);
                 SANIC_HIP(hipGetLastError());
             }
             std::vector<uint64_t> kargs;
@@ -219,7 +230,7 @@ static void enqueue(sanic_hip_exe* exe, const std::vector<sanic_hip_buffer*>& bo
                     kargs.push_back((uint64_t)(uintptr_t)b->ptr());
                     break;
                 }
-                case Arg::SCRATCH: kargs.push_back((uint64_t)(uintptr_t)(scratch + a.v)); break;
+                case Arg::SCRATCH: kargs.push_back((uint64_t)(uintptr_t)(arena + a.v)); break;
                 case Arg::IMM: kargs.push_back((uint64_t)a.v); break;
                 }
             }
@@ -314,6 +325,14 @@ int sanic_hip_open(int ordinal, sanic_hip_device** out) {
         SANIC_HIP(hipSetDevice(ordinal));
         SANIC_HIP(hipGetDeviceProperties(&d->props, ordinal));
         SANIC_HIP(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+        void* sp = nullptr;
+        hipError_t se = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+        if (se != hipSuccess || !sp) {
+            hipStreamDestroy(d->stream);
+            delete d;
+            fail(SANIC_ERR_BACKEND, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(se));
+        }
+        d->scratch_ptr = (char*)sp;
         *out = d;
     });
 }
@@ -492,6 +511,59 @@ int sanic_hip_execute(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int
             for (int i = 0; i < (int)exe->buffers.size(); i++)
                 if (bound[i] == o.get() && exe->buffers[i].role == SANIC_BUF_OUTPUT) outputs[i] = o.release();
         }
+    });
+}
+
+int sanic_hip_execute_static(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int n_bindings) {
+    return guarded([&] {
+        if (!exe || !bindings) fail(SANIC_ERR_ARG, "null argument");
+        for (int r : exe->stage_out_role)
+            if (r == SANIC_BUF_STATE)
+                fail(SANIC_ERR_IN_PLACE, "this program writes state in place; use capture (compile.rs:745-751)");
+        const int nb = (int)exe->buffers.size();
+        if (n_bindings != nb) fail(SANIC_ERR_ARG, "expected " + std::to_string(nb) + " bindings, got " + std::to_string(n_bindings));
+        char* base = exe->dev->scratch_ptr;
+        if (!base) fail(SANIC_ERR_BACKEND, "the device has no static scratch address");
+        // layout: the arena first, then every SCRATCH-role buffer, each at 256-byte alignment
+        auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
+        const int64_t arena = up(std::max<int64_t>(exe->low.scratch_bytes, 0));
+        int64_t need = arena;
+        std::vector<int64_t> at(nb, -1);
+        for (int i = 0; i < nb; i++)
+            if (exe->buffers[i].role == SANIC_BUF_SCRATCH) {
+                at[i] = need;
+                need += up(buffer_bytes(exe->buffers[i]));
+            }
+        if (need > (int64_t)kStaticScratchBytes)
+            fail(SANIC_ERR_ARG, "this program needs " + std::to_string(need) + " bytes of scratch; the static scratch holds " +
+                                    std::to_string(kStaticScratchBytes));
+        std::vector<sanic_hip_buffer> views(nb);
+        std::vector<sanic_hip_buffer*> bound(nb, nullptr);
+        auto whole = std::make_shared<Storage>();     // not owned: never freed
+        whole->ptr = base;
+        whole->bytes = kStaticScratchBytes;
+        for (int i = 0; i < nb; i++) {
+            if (at[i] >= 0) {
+                views[i].dev = exe->dev;
+                views[i].storage = whole;
+                views[i].offset = (size_t)at[i];
+                views[i].bytes = (size_t)buffer_bytes(exe->buffers[i]);
+                bound[i] = &views[i];
+            } else {
+                check_binding(exe, i, bindings[i]);
+                bound[i] = bindings[i];
+            }
+        }
+        SANIC_HIP(hipSetDevice(exe->dev->ordinal));
+        hipStream_t s = exe->dev->stream;
+        // arrival counters start at zero (a fill kernel, not a memset: safe under graph capture)
+        if (arena > 0) {
+            const int64_t words = arena / 4;
+            hipLaunchKernelGGL(sanic_zero_words, dim3((unsigned)std::min<int64_t>((words + 255) / 256, 4096)), dim3(256), 0, s,
+                               (uint32_t*)base, words);
+            SANIC_HIP(hipGetLastError());
+        }
+        enqueue(exe, bound, base);
     });
 }
 
