@@ -71,6 +71,18 @@ void emit_arrival(Code& k, const std::string& flag, const std::string& tid, cons
                   const std::string& expected);
 void validate(const sanic_program_desc* d);
 
+// The MI355X figures the cost model reads (the same numbers sanic_hip_specs reports).
+struct MachineSpecs {
+    double hbm, f32_flops, sram_bytes, regfile_bytes, launch, min_blocks, latency;
+};
+MachineSpecs mi355x_specs();
+// A generic fold's schedule: waves = 0 is the scalar form; split workgroups per point; chunk.
+struct FoldChoice {
+    int waves, split, chunk;
+    double time;
+};
+bool sched_is_auto(const sanic_sched& s);
+FoldChoice choose_fold_sched(const sanic_program_desc* d, const sanic_stage& st);
 LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& scratch, const std::vector<int>& tails);
 bool tail_candidate(const sanic_program_desc* d, int si);
 void emit_pointwise_loop(Renderer& R, Code& body, const sanic_program_desc* d, int si, const std::string& tid, int nth);

@@ -52,6 +52,12 @@ void emit_arrival(Code& k, const std::string& flag, const std::string& tid, cons
     k.line("__syncthreads();");
 }
 
+MachineSpecs mi355x_specs() {
+    // HBM3E peak; f32 VALU peak; LDS a workgroup may allocate; one CU's vector registers; the
+    // measured dependent-launch floor; 2 workgroups per CU fill the chip; loaded HBM latency
+    return {8.0e12, 157.3e12, 160.0 * 1024, 4 * 128.0 * 1024, 2.6e-6, 2.0 * 256, 2.0e-6};
+}
+
 int64_t dtype_bytes(int dt, int64_t n) {
     switch (dt) {
     case SANIC_F64: return 8 * n;
@@ -935,15 +941,130 @@ static void emit_finish(Renderer& R, Code& code, const sanic_stage& st, const st
     code.line(store_stmt(R.param(st.out_buffer), gid, st.out_dtype, v, false, R.d->buffers[st.out_buffer].scale));
 }
 
+// ── the default schedule of a generic fold (plan.rs:604-850 re-derived for wave64) ─────────
+//
+// A stage that carries no FoldSched (waves = 0, not lane_stream, split = 1) is priced over the
+// candidate schedules this emitter has, with the cost model of cost.rs:150-210 over the MI355X
+// figures sanic_hip_specs reports: time = max(compute / (f32 peak · occupancy), bytes /
+// sustainable bandwidth) + launch floor, sustainable bandwidth = peak · clamp(bytes in flight /
+// (peak · latency), 1/64, 1) (Little's law: lanes × bytes each lane keeps outstanding). The
+// candidates: scalar (one lane per output point); one workgroup of 64·w lanes per point (w =
+// 1..16) folding a strided stream; and s = 2..64 workgroups per point whose partial carriers the
+// last one merges. A split unit must not be empty (64·w·s ≤ stream). Ties go to the cooperative
+// form (lanes splitting the stream read consecutive elements, one cache line serving a whole
+// wave — a stated rule as in best_fold_sched, not a priced one); the winner's lanes then fold
+// contiguous runs of 8, 4 or 2 elements where the stream divides (more bytes in flight per load).
+static int64_t count_ops(const sanic_program_desc* d, int node, std::set<int>& seen) {
+    if (node < 0 || seen.count(node)) return 0;
+    seen.insert(node);
+    const sanic_node& n = d->nodes[node];
+    int64_t ops = n.kind == SANIC_NODE_CONST ? 0 : 1;
+    if (n.kind == SANIC_NODE_REDUCE || n.kind == SANIC_NODE_SCAN) {
+        // an in-body contraction re-issues its subtree once per contracted element
+        std::set<int> sub;
+        return ops + count_ops(d, n.in[0], sub) * std::max<int64_t>(1, d->nodes[n.in[0]].shape[n.dim]);
+    }
+    for (int k = 0; k < n.n_in; k++) ops += count_ops(d, n.in[k], seen);
+    return ops;
+}
+
+static int64_t expr_ops(const sanic_program_desc* d, int e) {
+    if (e < 0) return 0;
+    const sanic_expr& x = d->exprs[e];
+    if (x.op >= SANIC_EX_CONST) return 0;
+    return 1 + expr_ops(d, x.a) + expr_ops(d, x.b) + expr_ops(d, x.c);
+}
+
+static void collect_input_nodes(const sanic_program_desc* d, int node, std::set<int>& out) {
+    const sanic_node& n = d->nodes[node];
+    if (n.kind == SANIC_NODE_INPUT) out.insert(node);
+    for (int k = 0; k < n.n_in; k++) collect_input_nodes(d, n.in[k], out);
+}
+
+bool sched_is_auto(const sanic_sched& s) { return !s.lane_stream && s.waves == 0 && s.split <= 1; }
+
+FoldChoice choose_fold_sched(const sanic_program_desc* d, const sanic_stage& st) {
+    const MachineSpecs M = mi355x_specs();
+    const sanic_carrier& c = st.carrier;
+    const double gvol = (double)std::max<int64_t>(1, vol(st.grid, st.rank));
+    const double S = (double)std::max<int64_t>(1, st.stream);
+    // issue ops per (point, stream element): leaf evaluation + the slot updates
+    double per_el = 0;
+    std::set<int> seen;
+    for (int l = 0; l < st.n_leaves; l++) per_el += (double)count_ops(d, st.leaf[l], seen);
+    double slot_ops = 0;
+    for (int k = 0; k < c.slots; k++) slot_ops += (double)(expr_ops(d, c.into[k]) + expr_ops(d, c.combine[k]));
+    per_el += slot_ops;
+    // traffic: every input a leaf reads (once), plus the output; bytes a lane loads per stream
+    // step: the widths of the inputs whose leaf carries the streamed axis
+    double bytes = 0, streamed = 0;
+    std::set<int> bufs_seen;
+    for (int l = 0; l < st.n_leaves; l++) {
+        std::set<int> ins;
+        collect_input_nodes(d, st.leaf[l], ins);
+        bool streams = false;
+        for (int j = 0; j < d->nodes[st.leaf[l]].rank; j++) streams |= st.bind[l][j] == SANIC_BIND_STREAM;
+        for (int in : ins) {
+            const sanic_node& n = d->nodes[in];
+            const double w = (double)dtype_bytes(n.dtype, 1 << 10) / 1024.0;
+            if (streams) streamed += w;
+            if (bufs_seen.insert(n.buffer).second) bytes += (double)dtype_bytes(n.dtype, vol(n.shape, n.rank));
+        }
+    }
+    bytes += gvol * 4.0;
+    streamed = std::max(streamed, 1.0);
+    auto price = [&](int waves, int split, int chunk) -> double {
+        const bool scalar = waves == 0;
+        const double lanes_per_wg = scalar ? 256.0 : 64.0 * waves;
+        const double wgs = scalar ? std::ceil(gvol / 256.0) : gvol * split;
+        const double lds = scalar ? c.slots * 4.0 : waves * c.slots * 4.0;
+        const double regs = lanes_per_wg * c.slots * 4.0;
+        if (lds > M.sram_bytes || regs > M.regfile_bytes) return INFINITY;
+        double flops = gvol * S * per_el;
+        if (!scalar) flops += gvol * split * std::log2(64.0 * waves) * slot_ops + gvol * split * slot_ops;
+        const double resident = std::max(1.0, std::min({std::floor(M.sram_bytes / std::max(lds, 1.0)),
+                                                         std::floor(M.regfile_bytes / regs), wgs}));
+        const double occ = std::min(1.0, std::max(1.0 / 64.0, resident / M.min_blocks));
+        const double lanes = scalar ? gvol : wgs * lanes_per_wg;
+        const double in_flight = lanes * streamed * (scalar ? 1.0 : chunk);
+        const double bw = M.hbm * std::min(1.0, std::max(1.0 / 64.0, in_flight / (M.hbm * M.latency)));
+        return std::max(flops / (M.f32_flops * occ), bytes / bw) + M.launch * (split > 1 && gvol > 4096 ? 2 : 1);
+    };
+    FoldChoice best{0, 1, 1, price(0, 1, 1)};
+    for (int w : {1, 2, 4, 8, 16})
+        for (int sp : {1, 2, 4, 8, 16, 32, 64}) {
+            if (64.0 * w * sp > S) continue;            // an empty split unit would merge identity
+            const double t = price(w, sp, 1);
+            if (t < best.time || (t == best.time && best.waves == 0)) best = {w, sp, 1, t};
+        }
+    if (best.waves > 0)
+        for (int ch : {8, 4, 2})
+            if (st.stream % ((int64_t)64 * best.waves * best.split * ch) == 0) {
+                best.chunk = ch;
+                break;
+            }
+    return best;
+}
+
 LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& scratch, const std::vector<int>& tails) {
     const sanic_stage& st = d->stages[si];
     const sanic_carrier& c = st.carrier;
     LoweredStage L;
     int64_t gvol = vol(st.grid, st.rank);
     auto win = honest_window(d, st);
-    int split = st.sched.split > 1 ? (int)std::min<int64_t>(st.sched.split, st.stream) : 1;
-    int waves = st.sched.lane_stream ? std::max(1, std::min(16, st.sched.waves)) : 0;
-    int chunk = std::max(1, st.sched.chunk);
+    sanic_sched sch = st.sched;
+    std::string auto_tag;
+    if (sched_is_auto(sch)) {
+        const FoldChoice fc = choose_fold_sched(d, st);
+        sch.lane_stream = fc.waves > 0;
+        sch.waves = fc.waves;
+        sch.split = fc.split;
+        sch.chunk = fc.chunk;
+        auto_tag = "[auto w" + std::to_string(fc.waves) + " s" + std::to_string(fc.split) + " c" + std::to_string(fc.chunk) + "]";
+    }
+    int split = sch.split > 1 ? (int)std::min<int64_t>(sch.split, st.stream) : 1;
+    int waves = sch.lane_stream ? std::max(1, std::min(16, sch.waves)) : 0;
+    int chunk = std::max(1, sch.chunk);
     Renderer R(d);
     for (int t : tails) R.coherent.insert(d->stages[t].out_buffer);
     if (!tails.empty()) R.coherent.insert(st.out_buffer);   // tails may read the merged result
@@ -957,7 +1078,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     };
 
     if (waves == 0 && split == 1) {
-        L.kernel_kind = "fold:scalar";
+        L.kernel_kind = "fold:scalar" + auto_tag;
         body.line("const idx_t gid = (idx_t)blockIdx.x * 256 + threadIdx.x;");
         body.line("if (gid >= " + std::to_string(gvol) + ") return;");
         decode_grid(body, st, "gid");
@@ -980,7 +1101,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     // cooperative / split: one workgroup of `nth` lanes folds one (grid point, split slice)
     int nth = 64 * std::max(1, waves);
     int nw = nth / 64;
-    L.kernel_kind = split > 1 ? "fold:split" : "fold:coop";
+    L.kernel_kind = (split > 1 ? "fold:split" : "fold:coop") + auto_tag;
     int64_t part_off = scratch;
     const bool fused_merge = split > 1 && gvol <= 4096;
     const int64_t part_bytes = ((gvol * split * c.slots * 4 + 255) / 256) * 256;
@@ -1148,7 +1269,7 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
         std::vector<Arg> args = R.arg_list();
         args.push_back({Arg::SCRATCH, part_off});
         L.launches.push_back({"sanic_fold_split", "", dim3((unsigned)(gvol * split)), dim3(nth), 0, args});
-        L.kernel_kind = "fold:split+merge" + std::string(tails.empty() ? "" : "+tail" + std::to_string(tails.size()));
+        L.kernel_kind = "fold:split+merge" + auto_tag + std::string(tails.empty() ? "" : "+tail" + std::to_string(tails.size()));
         L.source = src.str();
         return L;
     }

@@ -360,11 +360,12 @@ int sanic_hip_specs(sanic_hip_device* dev, sanic_device_specs* out) {
         out->f32_flops = 157.3e12;
         out->clock_hz = dev->props.clockRate * 1000.0;
         out->hbm_bytes = (int64_t)dev->props.totalGlobalMem;
-        out->sram_bytes = 160.0 * 1024;
-        out->regfile_bytes = 4 * 128.0 * 1024;
-        out->launch_overhead_s = 2.6e-6;
+        const MachineSpecs m = mi355x_specs();
+        out->sram_bytes = m.sram_bytes;
+        out->regfile_bytes = m.regfile_bytes;
+        out->launch_overhead_s = m.launch;
         out->min_blocks = 2.0 * out->compute_units;
-        out->mem_latency_s = 2.0e-6;
+        out->mem_latency_s = m.latency;
     });
 }
 

@@ -25,7 +25,9 @@ STREAM, BCAST = -1, -2
 class Sched:
     """FoldSched re-derived for wave64: `lane_stream` lanes split the stream, `waves`
     wavefronts per workgroup, `chunk` contiguous elements per lane, `split` workgroups per
-    output point merged by the carrier's combine (split-K / Flash-Decoding)."""
+    output point merged by the carrier's combine (split-K / Flash-Decoding). A stage built
+    without a Sched carries `waves = 0` (not lane_stream, split 1): the backend prices its
+    candidate schedules and picks one (plan.rs:604-850); `Sched()` itself is the scalar form."""
     lane_stream: bool = False
     waves: int = 1
     chunk: int = 1
@@ -103,7 +105,7 @@ class Program:
         out = self._decl(name, role, grid, out_dtype)
         lv = [(n, tuple(b)) for n, b in leaves]
         self.stages.append(Stage(0, name, out, tuple(grid), int(stream), lv, carrier, epilogue,
-                                 sched or Sched()))
+                                 sched or Sched(waves=0)))
         return self.node(name)
 
     def pointwise(self, name: str, value: ir.Node, out_dtype=ir.F32, grid=None,

@@ -42,11 +42,13 @@ def test_open_without_gpu_reports_backend_error():
     assert st == 6 and not h.value   # SANIC_ERR_BACKEND (MetalDevice::open → None)
 
 
-@pytest.mark.parametrize("name", ["A", "A_coop", "A_split", "B1", "B1_rows", "B2", "D1", "D2", "C1", "C3",
+@pytest.mark.parametrize("name", ["A", "A_scalar", "A_coop", "A_split", "B1", "B1_rows", "B2", "D1", "D2", "C1", "C3",
                                   "E_qkv", "E_attn", "E_gateup"])
 def test_lowering_chooses_the_expected_kernel(name):
     progs = {
-        "A": (configs.direct_attention(), 0, "fold:scalar"),
+        # no Sched: the priced default (one wave per point, runs of 2)
+        "A": (configs.direct_attention(), 0, "fold:coop[auto w1 s1 c2]"),
+        "A_scalar": (configs.direct_attention(sched=Sched()), 0, "fold:scalar"),
         "A_coop": (configs.direct_attention(sched=Sched(lane_stream=True, waves=2)), 0, "fold:coop"),
         "A_split": (configs.direct_attention(sched=Sched(lane_stream=True, waves=2, split=4)), 0, "fold:split"),
         "B1": (configs.rmsnorm_projection(kmajor=True), 0, "skeleton:gemv_kmajor"),

@@ -11,7 +11,8 @@ from tests.util import max_rel_err, run_on_gpu
 pytestmark = pytest.mark.gpu
 
 SCHEDS = {
-    "scalar": None,
+    "auto": None,
+    "scalar": Sched(),
     "coop1": Sched(lane_stream=True, waves=1),
     "coop4_chunk2": Sched(lane_stream=True, waves=4, chunk=2),
     "split4": Sched(lane_stream=True, waves=2, split=4),
@@ -141,3 +142,19 @@ def test_split_merge_butterfly_small_grid_attention(dev):
     assert exe.stage_kernel(0).startswith("fold:split+merge")
     want = oracle.run_program(prog, vals)["O"]
     assert max_rel_err(got["O"], want) < 1e-4
+
+
+@pytest.mark.parametrize("grid,stream", [(1, 1 << 20), (3, 700001), (128, 128256)])
+def test_default_schedule_long_stream_small_grid(dev, grid, stream):
+    """A stage built without a Sched: the backend prices its schedules (plan.rs:604-850) and
+    splits a long stream over a small grid across workgroups; the sums match the oracle."""
+    p = Program()
+    x = p.input("x", (grid, stream), ir.F32)
+    p.fused("y", (grid,), stream, [(x, (0, STREAM))], C.plain(ir.M_ADD))
+    vals = {"x": oracle.lcg(grid + stream, grid * stream).reshape(grid, stream)}
+    got, exe = run_on_gpu(dev, p, vals)
+    assert exe.stage_kernel(0).startswith("fold:split+merge[auto"), exe.stage_kernel(0)
+    want = oracle.run_program(p, vals)["y"]
+    err = max_rel_err(got["y"], want)
+    print(exe.stage_kernel(0), err)
+    assert err < 1e-4
