@@ -1378,7 +1378,13 @@ Lowered lower_program(const sanic_program_desc* d) {
             std::vector<int> tails;
             int64_t gv = 1;
             for (int j = 0; j < st.rank; j++) gv *= st.grid[j];
-            if (st.sched.lane_stream && st.sched.split > 1 && std::min<int64_t>(st.sched.split, st.stream) > 1 && gv <= 4096)
+            sanic_sched es = st.sched;
+            if (sched_is_auto(es)) {
+                const FoldChoice fc = choose_fold_sched(d, st);
+                es.lane_stream = fc.waves > 0;
+                es.split = fc.split;
+            }
+            if (es.lane_stream && es.split > 1 && std::min<int64_t>(es.split, st.stream) > 1 && gv <= 4096)
                 for (int t = s + 1; tail_candidate(d, t) && !stage_touches_q8(d, t) && tails.size() < 4; t++) tails.push_back(t);
             L = lower_generic_fold(d, s, out.scratch_bytes, tails);
             out.stages.push_back(std::move(L));
