@@ -484,19 +484,22 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         c2.indent--;
         c2.line("}");
     };
+    // one K tile's MFMAs: every operand fragment of both 32-deep halves is read from LDS first,
+    // then the MFMAs issue, so the second half's reads complete under the first half's MFMAs
+    // (with one wave per SIMD nothing else hides the LDS latency)
     auto emit_mfma = [&](Code& c2, const std::string& buf) {
-        c2.line("#pragma unroll");
-        c2.line("for (int ks = 0; ks < 2; ++ks) {");
         const std::string MTs = std::to_string(MT), NTs = std::to_string(NT);
         const std::string aidx = "[" + koff("wm + i * 16 + l16", "ks * 32 + lq * 8", AS) + "]";
-        const std::string bidx = "[" + koff("wn + j * 16 + l16", "ks * 32 + lq * 8", BS) + "]";
-        c2.line("  bf16x8 af[" + MTs + "], bf[" + NTs + "];");
-        if (splitA) c2.line("  bf16x8 afl[" + MTs + "];");
-        if (splitB) c2.line("  bf16x8 bfl[" + NTs + "];");
+        c2.line("{");
+        c2.line("bf16x8 af[2][" + MTs + "], bf[2][" + NTs + "];");
+        if (splitA) c2.line("bf16x8 afl[2][" + MTs + "];");
+        if (splitB) c2.line("bf16x8 bfl[2][" + NTs + "];");
+        c2.line("#pragma unroll");
+        c2.line("for (int ks = 0; ks < 2; ++ks) {");
         c2.line("  #pragma unroll");
         c2.line("  for (int i = 0; i < " + MTs + "; ++i) {");
-        c2.line("    af[i] = *(const bf16x8*)(&a_lds[" + buf + "]" + aidx + ");");
-        if (splitA) c2.line("    afl[i] = *(const bf16x8*)(&a_lo[" + buf + "]" + aidx + ");");
+        c2.line("    af[ks][i] = *(const bf16x8*)(&a_lds[" + buf + "]" + aidx + ");");
+        if (splitA) c2.line("    afl[ks][i] = *(const bf16x8*)(&a_lo[" + buf + "]" + aidx + ");");
         c2.line("  }");
         c2.line("  #pragma unroll");
         c2.line("  for (int j = 0; j < " + NTs + "; ++j) {");
@@ -512,20 +515,26 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
                 c2.line("      " + dst + " = __builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(t0_, t1_, 0, 1, 2, 3, 4, 5, 6, 7));");
                 c2.line("    }");
             };
-            tr("b_lds", "bf[j]");
-            if (splitB) tr("b_lo", "bfl[j]");
+            tr("b_lds", "bf[ks][j]");
+            if (splitB) tr("b_lo", "bfl[ks][j]");
         } else {
-            c2.line("    bf[j] = *(const bf16x8*)(&b_lds[" + buf + "]" + bidx + ");");
-            if (splitB) c2.line("    bfl[j] = *(const bf16x8*)(&b_lo[" + buf + "]" + bidx + ");");
+            const std::string bidx = "[" + koff("wn + j * 16 + l16", "ks * 32 + lq * 8", BS) + "]";
+            c2.line("    bf[ks][j] = *(const bf16x8*)(&b_lds[" + buf + "]" + bidx + ");");
+            if (splitB) c2.line("    bfl[ks][j] = *(const bf16x8*)(&b_lo[" + buf + "]" + bidx + ");");
         }
         c2.line("  }");
+        c2.line("}");
+        // the scheduler would sink each read to its first use
+        c2.line("__builtin_amdgcn_sched_barrier(0);");
+        c2.line("#pragma unroll");
+        c2.line("for (int ks = 0; ks < 2; ++ks)");
         c2.line("  #pragma unroll");
         c2.line("  for (int i = 0; i < " + MTs + "; ++i)");
         c2.line("    #pragma unroll");
         c2.line("    for (int j = 0; j < " + NTs + "; ++j) {");
-        c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);");
-        if (splitA) c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afl[i], bf[j], acc[i][j], 0, 0, 0);");
-        if (splitB) c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfl[j], acc[i][j], 0, 0, 0);");
+        c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);");
+        if (splitA) c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afl[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);");
+        if (splitB) c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks][i], bfl[ks][j], acc[i][j], 0, 0, 0);");
         c2.line("    }");
         c2.line("}");
     };

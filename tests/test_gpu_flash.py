@@ -44,20 +44,25 @@ def _round_bf16_array(x):
 
 
 @pytest.mark.parametrize("window", [0, 1024])
-def test_flash_full_size_heads_subset(dev, window):
-    """Config C1 (causal) / C2 (1024-token window) at full size: heads 0, 13 and 31 against the
-    fused f64 attention over the same RoPE'd, bf16-rounded Q and K."""
+def test_flash_full_size_all_heads(dev, window):
+    """Config C1 (causal) / C2 (1024-token window) at full size: all 32 query heads against the
+    fused f64 attention over the same RoPE'd, bf16-rounded Q and K. Every head is checked, since
+    the kernel remaps blockIdx to (KV head, query head, query block) for XCD locality and a
+    mapping error would touch only some heads."""
     NH, NKV, S, HD = 32, 8, 4096, 64
     prog = configs.flash_prefill(NH, NKV, S, window=window)
     vals = _inputs(NH, NKV, S, seed=500)
     got, exe = run_on_gpu(dev, prog, vals)
     invf = oracle.inv_freq(500000.0, HD // 2)
     kr = _round_bf16_array(oracle.rope(vals["K"], 0, invf))
-    for h in (0, 13, 31):
-        qr = _round_bf16_array(oracle.rope(vals["Q"][h:h + 1], 0, invf))
-        kv = h // (NH // NKV)
-        want = oracle.attention(qr, kr[kv:kv + 1], vals["V"][kv:kv + 1], 1.0 / 8.0,
-                                mask=2 if window else 1, window=window)
-        err = max_rel_err(got["O"][h:h + 1], want)
-        print(exe.stage_kernel(2), window, h, err)
-        assert err < 2e-2
+    qr = _round_bf16_array(oracle.rope(vals["Q"], 0, invf))
+    want = oracle.attention(qr, kr, vals["V"], 1.0 / 8.0, mask=2 if window else 1, window=window)
+    per_head = [max_rel_err(got["O"][h], want[h]) for h in range(NH)]
+    # the floored relative form, printed so that a regression on small outputs shows even where
+    # the reference's metric (closer to an absolute bound near zero) still passes
+    g, e = np.asarray(got["O"], np.float64), want
+    floored = float(np.max(np.abs(g - e) / np.maximum(np.abs(e), 1e-3)))
+    print(exe.stage_kernel(2), window, f"max |g-e|/(1+|e|) {max(per_head):.3e}",
+          f"max |g-e|/max(|e|,1e-3) {floored:.3e}")
+    bad = [h for h, err in enumerate(per_head) if not err < 2e-2]
+    assert not bad, [(h, per_head[h]) for h in bad]
