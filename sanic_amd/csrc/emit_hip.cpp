@@ -37,9 +37,10 @@ static int64_t vol(const int64_t* s, int r) {
 static std::vector<int64_t> shp(const sanic_node& n) { return {n.shape, n.shape + n.rank}; }
 
 // Ordering (HIP's scoped memory model): every thread's partial stores happen before the
-// barrier (workgroup scope), the barrier before thread 0's agent-scope release RMW, which
-// synchronises with the last arriver's acquire RMW on the same counter, which happens before
-// that workgroup's barrier and so before every one of its threads reads the partials. The
+// barrier (workgroup scope), the barrier before thread 0's agent-scope release RMW. The last
+// arriver's RMW reads the release sequence of every earlier arrival, and its agent-scope
+// acquire fence after the RMW synchronises with all of them; the fence happens before that
+// workgroup's barrier and so before every one of its threads reads the partials. The
 // waitcnt makes each wave's own stores complete before the barrier, so the release has nothing
 // of theirs left in flight.
 void emit_arrival(Code& k, const std::string& flag, const std::string& tid, const std::string& cnt,
@@ -47,8 +48,13 @@ void emit_arrival(Code& k, const std::string& flag, const std::string& tid, cons
     k.line("__shared__ int " + flag + ";");
     k.line("__builtin_amdgcn_s_waitcnt(0);");
     k.line("__syncthreads();");
-    k.line("if (" + tid + " == 0) " + flag + " = __hip_atomic_fetch_add(" + cnt +
-           ", 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (" + expected + ") - 1u;");
+    // release on every arrival; only the last arriver, which goes on to read the others'
+    // partials, takes the acquire (a fence after its RMW, which reads the release sequence of
+    // every earlier arrival) — the others skip the acquire's cache invalidation
+    k.line("if (" + tid + " == 0) {");
+    k.line("  " + flag + " = __hip_atomic_fetch_add(" + cnt + ", 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == (" + expected + ") - 1u;");
+    k.line("  if (" + flag + ") __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, \"agent\");");
+    k.line("}");
     k.line("__syncthreads();");
 }
 
