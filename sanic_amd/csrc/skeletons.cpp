@@ -729,9 +729,13 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         const int KIq = (int)(KQ / 512);
         const int NSEG = (int)group.size();
         // rows per workgroup: 4 for very tall matrices (lm_head: fewer, fuller workgroups
-        // measured faster), else 2 (the measured tuner's pick for the 2048×8192 down
-        // projection in the decode step: 680 → 655 µs per step against 4)
-        int RBI = NTOT >= 65536 ? 4 : 2;
+        // measured faster) and for packed 4-bit weights (a lane's run of 8 weights is 4 bytes,
+        // so more rows keep more bytes in flight: int4 8192×2048 5.37 → 5.09 µs, 8 rows 5.75),
+        // else 2 (the measured tuner's pick for the 2048×8192 down projection in the decode
+        // step: 680 → 655 µs per step against 4)
+        bool packed4 = false;
+        for (int dt : wd0) packed4 |= dt == SANIC_U4 || dt == SANIC_I4;
+        int RBI = NTOT >= 65536 || packed4 ? 4 : 2;
         // tiling variants for the measured tuner: rows per workgroup {rule, 1, 2, 4} ({2, 1, 4}
         // for a paired launch, whose workgroup holds row i of every segment)
         const int gvar = d->stages[si].sched.variant;
