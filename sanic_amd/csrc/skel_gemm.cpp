@@ -8,8 +8,8 @@
 // slot: A = rest, B = W, both rounded to bf16 for the MFMA) or free of W (a row slot: Σx² of a
 // fused RMSNorm, folded per row in f32 alongside the A tile).
 //
-// Kernel shape: workgroup tile BM × BN (4 waves in 2 × 2, each (BM/2) × (BN/2) of 16×16 MFMA
-// tiles), K in 64-wide steps, A and B tiles double-buffered in LDS with k contiguous so every
+// Kernel shape: workgroup tile BM × BN (8 waves in 4 × 2 for 128-row tiles at least 64 columns
+// wide, else 4 waves in 2 × 2; each wave a block of 16×16 MFMA tiles), K in 64-wide steps, A and B tiles double-buffered in LDS with k contiguous so every
 // MFMA operand is one ds_read_b128; the weight leaf is loaded by the vector renderer (128-bit
 // runs of 8 along k, per-group scale/zero once per run, packed nibbles decoded in registers);
 // project, epilogue and the narrowing store per output element.
@@ -171,7 +171,11 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     int BN = 128;
     while (BN > 32 && (M / BM) * (N / BN) < 256) BN /= 2;
     if (N % BN) return false;
-    const int WM = BM / 2, WN = BN / 2;       // per-wave tile
+    // 8 waves (4 × 2, two per SIMD) when the tile is 128 rows and at least 64 columns, so one
+    // wave's LDS operand reads and global loads proceed under the other's MFMAs; else 4 (2 × 2)
+    const int NTH = (BM == 128 && BN >= 64) ? 512 : 256;
+    const int WGM = NTH / 128;                // waves along m (2 along n)
+    const int WM = BM / WGM, WN = BN / 2;     // per-wave tile
     const int MT = WM / 16, NT = WN / 16;
     const int SR = (int)P.rslots.size();
     int AS = 64 + 8;                          // LDS row strides (bf16)
@@ -342,13 +346,13 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     k.line("  for (int j = 0; j < " + std::to_string(NT) + "; ++j) acc[i][j] = (f32x4){0, 0, 0, 0};");
     for (int i = 0; i < SR; i++) k.line("float racc" + std::to_string(i) + " = 0.0f;");
 
-    // A tile: BM rows × 64 k; thread t owns row (t·BM/256)… with 256/BM threads per row, each
-    // a contiguous run of 64·BM/256 k in runs of 8
-    const int TPR = 256 / BM;              // threads per row: 2 (BM 128) or 4 (BM 64)
+    // A tile: BM rows × 64 k; NTH/BM consecutive threads per row, each a contiguous run of
+    // 64·BM/NTH k in runs of 8
+    const int TPR = NTH / BM;              // threads per row: 4 (BM 128 at 512 threads, BM 64 at 256)
     const int RUNS_A = 64 / TPR / 8;       // runs of 8 per thread per tile
     // B tile: BN n × 64 k = BN·8 runs; k-contiguous weights: 8 lanes per row (coalesced rows),
     // else adjacent lanes take adjacent n
-    const int RUNS_B = BN * 8 / 256;
+    const int RUNS_B = BN * 8 / NTH;
     auto emit_loads = [&](Code& c2, const std::string& kt0, const std::string& sfx) {
         // A runs
         c2.line("const idx_t mm" + sfx + " = m0 + tid / " + std::to_string(TPR) + ";");
@@ -383,15 +387,15 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             std::string nn, kk;
             if (bkn) {
                 // chunk c = tid + 256·r: k row c / (BN/8), 8 columns from (c % (BN/8))·8
-                const std::string cc = "(tid + " + std::to_string(r * 256) + ")";
+                const std::string cc = "(tid + " + std::to_string(r * NTH) + ")";
                 kk = "(" + kt0 + " + " + cc + " / " + std::to_string(BN / 8) + ")";
                 nn = "(n0 + (" + cc + " % " + std::to_string(BN / 8) + ") * 8)";
             } else if (contig) {
-                nn = "(n0 + (tid / 8) + " + std::to_string(r * 32) + ")";
+                nn = "(n0 + (tid / 8) + " + std::to_string(r * (NTH / 8)) + ")";
                 kk = "(" + kt0 + " + (tid % 8) * 8)";
             } else {
                 nn = "(n0 + (tid % " + std::to_string(BN) + "))";
-                kk = "(" + kt0 + " + ((tid / " + std::to_string(BN) + ") + " + std::to_string(r * (256 / BN)) + ") * 8)";
+                kk = "(" + kt0 + " + ((tid / " + std::to_string(BN) + ") + " + std::to_string(r * (NTH / BN)) + ") * 8)";
             }
             std::vector<int> rb, rd;
             bool rok = true, rc = true;
@@ -466,16 +470,16 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             std::string row, col;
             int stride = BS;
             if (bkn) {
-                const std::string cc = "(tid + " + std::to_string(r * 256) + ")";
+                const std::string cc = "(tid + " + std::to_string(r * NTH) + ")";
                 row = "(" + cc + " / " + std::to_string(BN / 8) + ")";
                 col = "((" + cc + " % " + std::to_string(BN / 8) + ") * 8)";
                 stride = BNS;
             } else if (contig) {
-                row = "((tid / 8) + " + std::to_string(r * 32) + ")";
+                row = "((tid / 8) + " + std::to_string(r * (NTH / 8)) + ")";
                 col = "((tid % 8) * 8)";
             } else {
                 row = "(tid % " + std::to_string(BN) + ")";
-                col = "(((tid / " + std::to_string(BN) + ") + " + std::to_string(r * (256 / BN)) + ") * 8)";
+                col = "(((tid / " + std::to_string(BN) + ") + " + std::to_string(r * (NTH / BN)) + ") * 8)";
             }
             const std::string boff = bkn ? row + " * " + std::to_string(stride) + " + " + col : koff(row, col, stride);
             c2.line("*(sanic_u32x4*)(&b_lds[" + buf + "][" + boff + "]) = rb" + rs + sfx + ";");
@@ -634,7 +638,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     }
     // row slots: sum the TPR partial rows, publish per row
     if (SR && pre) {
-        k.line("for (int i = tid; i < " + std::to_string(BM * SR) + "; i += 256) rs_lds[i] = ((const float*)((const char*)a.scratch + " + std::to_string(rs_off) +
+        k.line("for (int i = tid; i < " + std::to_string(BM * SR) + "; i += " + std::to_string(NTH) + ") rs_lds[i] = ((const float*)((const char*)a.scratch + " + std::to_string(rs_off) +
                "))[m0 * " + std::to_string(SR) + " + i];");
         k.line("__syncthreads();");
     }
@@ -697,7 +701,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
            "  lo = pk_bf16(x - __uint_as_float(h << 16), y - __uint_as_float(h & 0xFFFF0000u));\n}\n";
     src << R.args_struct(pre ? std::vector<std::string>{"float* __restrict__ scratch"} : std::vector<std::string>{});
     if (pre) src << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "_pre(Args a) {\n" << R.entry() << kp.str() << "}\n";
-    src << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(" << NTH << ") " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     out.kernel_kind = "skeleton:gemm[" + std::to_string(BM) + "x" + std::to_string(BN) + (splitA ? ",a2" : "") + (splitB ? ",b2" : "") + (bkn ? ",kn" : "") + (pre ? ",pre" : "") + "]";
     out.source = src.str();
     std::vector<Arg> args = R.arg_list();
@@ -705,7 +709,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         args.push_back({Arg::SCRATCH, 0});
         out.launches.push_back({kname + "_pre", "", dim3((unsigned)(M / 4)), dim3(256), 0, args});
     }
-    out.launches.push_back({kname, "", dim3((unsigned)((M / BM) * (N / BN))), dim3(256), 0, args});
+    out.launches.push_back({kname, "", dim3((unsigned)((M / BM) * (N / BN))), dim3(NTH), 0, args});
     return true;
 }
 
