@@ -488,58 +488,76 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         c2.indent--;
         c2.line("}");
     };
-    // one K tile's MFMAs: every operand fragment of both 32-deep halves is read from LDS first,
-    // then the MFMAs issue, so the second half's reads complete under the first half's MFMAs
-    // (with one wave per SIMD nothing else hides the LDS latency)
+    // one K tile's MFMAs over its two 32-deep halves: the first half's operand fragments are
+    // read from LDS, then the second half's reads are interleaved one by one with the first
+    // half's MFMAs (scheduling groups), then the second half's MFMAs — so LDS reads proceed
+    // under MFMAs within each wave as well as across the two waves of a SIMD (8-wave tiles:
+    // 44.5 → 41.7 µs for B2's GEMM against reading everything first)
     auto emit_mfma = [&](Code& c2, const std::string& buf) {
         const std::string MTs = std::to_string(MT), NTs = std::to_string(NT);
-        const std::string aidx = "[" + koff("wm + i * 16 + l16", "ks * 32 + lq * 8", AS) + "]";
         c2.line("{");
         c2.line("bf16x8 af[2][" + MTs + "], bf[2][" + NTs + "];");
         if (splitA) c2.line("bf16x8 afl[2][" + MTs + "];");
         if (splitB) c2.line("bf16x8 bfl[2][" + NTs + "];");
-        c2.line("#pragma unroll");
-        c2.line("for (int ks = 0; ks < 2; ++ks) {");
-        c2.line("  #pragma unroll");
-        c2.line("  for (int i = 0; i < " + MTs + "; ++i) {");
-        c2.line("    af[ks][i] = *(const bf16x8*)(&a_lds[" + buf + "]" + aidx + ");");
-        if (splitA) c2.line("    afl[ks][i] = *(const bf16x8*)(&a_lo[" + buf + "]" + aidx + ");");
-        c2.line("  }");
-        c2.line("  #pragma unroll");
-        c2.line("  for (int j = 0; j < " + NTs + "; ++j) {");
-        if (bkn) {
-            // rows ks·32 + lq·8 + (0..3 | 4..7), column wn + j·16 + l16: in each 16-lane group,
-            // source lane s reads 4 columns 4·(s%4) of row base + s/4; lane i gets 4 rows of column i
-            const std::string br = "[(ks * 32 + lq * 8 + (l16 >> 2)) * " + std::to_string(BNS) + " + wn + j * 16 + (l16 & 3) * 4]";
-            auto tr = [&](const std::string& arr, const std::string& dst) {
-                c2.line("    {");
-                c2.line("      const unsigned short* bp = &" + arr + "[" + buf + "]" + br + ";");
-                c2.line("      const sanic_s16x4 t0_ = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(bp));");
-                c2.line("      const sanic_s16x4 t1_ = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(bp + 4 * " + std::to_string(BNS) + "));");
-                c2.line("      " + dst + " = __builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(t0_, t1_, 0, 1, 2, 3, 4, 5, 6, 7));");
-                c2.line("    }");
-            };
-            tr("b_lds", "bf[ks][j]");
-            if (splitB) tr("b_lo", "bfl[ks][j]");
-        } else {
-            const std::string bidx = "[" + koff("wn + j * 16 + l16", "ks * 32 + lq * 8", BS) + "]";
-            c2.line("    bf[ks][j] = *(const bf16x8*)(&b_lds[" + buf + "]" + bidx + ");");
-            if (splitB) c2.line("    bfl[ks][j] = *(const bf16x8*)(&b_lo[" + buf + "]" + bidx + ");");
-        }
-        c2.line("  }");
-        c2.line("}");
-        // the scheduler would sink each read to its first use
+        auto reads = [&](int ks) {
+            const std::string kss = std::to_string(ks);
+            const std::string aidx = "[" + koff("wm + i * 16 + l16", kss + " * 32 + lq * 8", AS) + "]";
+            c2.line("#pragma unroll");
+            c2.line("for (int i = 0; i < " + MTs + "; ++i) {");
+            c2.line("  af[" + kss + "][i] = *(const bf16x8*)(&a_lds[" + buf + "]" + aidx + ");");
+            if (splitA) c2.line("  afl[" + kss + "][i] = *(const bf16x8*)(&a_lo[" + buf + "]" + aidx + ");");
+            c2.line("}");
+            c2.line("#pragma unroll");
+            c2.line("for (int j = 0; j < " + NTs + "; ++j) {");
+            if (bkn) {
+                // rows ks·32 + lq·8 + (0..3 | 4..7), column wn + j·16 + l16: in each 16-lane
+                // group, source lane s reads 4 columns 4·(s%4) of row base + s/4; lane i gets 4
+                // rows of column i
+                const std::string br = "[(" + kss + " * 32 + lq * 8 + (l16 >> 2)) * " + std::to_string(BNS) + " + wn + j * 16 + (l16 & 3) * 4]";
+                auto tr = [&](const std::string& arr, const std::string& dst) {
+                    c2.line("  {");
+                    c2.line("    const unsigned short* bp = &" + arr + "[" + buf + "]" + br + ";");
+                    c2.line("    const sanic_s16x4 t0_ = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(bp));");
+                    c2.line("    const sanic_s16x4 t1_ = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(bp + 4 * " + std::to_string(BNS) + "));");
+                    c2.line("    " + dst + " = __builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(t0_, t1_, 0, 1, 2, 3, 4, 5, 6, 7));");
+                    c2.line("  }");
+                };
+                tr("b_lds", "bf[" + kss + "][j]");
+                if (splitB) tr("b_lo", "bfl[" + kss + "][j]");
+            } else {
+                const std::string bidx = "[" + koff("wn + j * 16 + l16", kss + " * 32 + lq * 8", BS) + "]";
+                c2.line("  bf[" + kss + "][j] = *(const bf16x8*)(&b_lds[" + buf + "]" + bidx + ");");
+                if (splitB) c2.line("  bfl[" + kss + "][j] = *(const bf16x8*)(&b_lo[" + buf + "]" + bidx + ");");
+            }
+            c2.line("}");
+        };
+        auto mfmas = [&](int ks) {
+            const std::string kss = std::to_string(ks);
+            c2.line("#pragma unroll");
+            c2.line("for (int i = 0; i < " + MTs + "; ++i)");
+            c2.line("  #pragma unroll");
+            c2.line("  for (int j = 0; j < " + NTs + "; ++j) {");
+            c2.line("    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[" + kss + "][i], bf[" + kss + "][j], acc[i][j], 0, 0, 0);");
+            if (splitA) c2.line("    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afl[" + kss + "][i], bf[" + kss + "][j], acc[i][j], 0, 0, 0);");
+            if (splitB) c2.line("    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[" + kss + "][i], bfl[" + kss + "][j], acc[i][j], 0, 0, 0);");
+            c2.line("  }");
+        };
+        // instruction counts of one half: LDS reads and MFMAs
+        const int nds = MT * (splitA ? 2 : 1) + NT * (bkn ? 2 : 1) * (splitB ? 2 : 1);
+        const int nmf = MT * NT * (1 + (splitA ? 1 : 0) + (splitB ? 1 : 0));
+        reads(0);
         c2.line("__builtin_amdgcn_sched_barrier(0);");
-        c2.line("#pragma unroll");
-        c2.line("for (int ks = 0; ks < 2; ++ks)");
-        c2.line("  #pragma unroll");
-        c2.line("  for (int i = 0; i < " + MTs + "; ++i)");
-        c2.line("    #pragma unroll");
-        c2.line("    for (int j = 0; j < " + NTs + "; ++j) {");
-        c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);");
-        if (splitA) c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afl[ks][i], bf[ks][j], acc[i][j], 0, 0, 0);");
-        if (splitB) c2.line("      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks][i], bfl[ks][j], acc[i][j], 0, 0, 0);");
-        c2.line("    }");
+        reads(1);
+        mfmas(0);
+        const int pairs = std::min(nds, nmf);
+        for (int i = 0; i < pairs; i++) {
+            c2.line("__builtin_amdgcn_sched_group_barrier(0x008, 1, 0);");   // one MFMA
+            c2.line("__builtin_amdgcn_sched_group_barrier(0x100, 1, 0);");   // one LDS read
+        }
+        if (nmf > pairs) c2.line("__builtin_amdgcn_sched_group_barrier(0x008, " + std::to_string(nmf - pairs) + ", 0);");
+        if (nds > pairs) c2.line("__builtin_amdgcn_sched_group_barrier(0x100, " + std::to_string(nds - pairs) + ", 0);");
+        c2.line("__builtin_amdgcn_sched_barrier(0);");
+        mfmas(1);
         c2.line("}");
     };
     const int64_t NKT = K / 64;
