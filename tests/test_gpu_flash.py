@@ -4,7 +4,7 @@ import pytest
 
 import oracle
 from sanic_amd import configs, ir
-from tests.util import max_rel_err, run_on_gpu
+from tests.util import floored_rel_err, max_rel_err, run_on_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -27,7 +27,7 @@ def test_flash_small_matches_interpreter_schedule(dev, window):
     # bf16 output: the reference's GPU metric |g − e| / (1 + |e|) (tests/metal.rs:99-105) at the
     # bf16 bound; attention outputs straddle zero, so a relative-to-|e| metric would not apply
     err = max_rel_err(got["O"], want["O"])
-    print(exe.stage_kernel(2), window, err)
+    print(exe.stage_kernel(2), window, err, floored_rel_err(got["O"], want["O"]))
     assert err < 2e-2
 
 
@@ -58,10 +58,7 @@ def test_flash_full_size_all_heads(dev, window):
     qr = _round_bf16_array(oracle.rope(vals["Q"], 0, invf))
     want = oracle.attention(qr, kr, vals["V"], 1.0 / 8.0, mask=2 if window else 1, window=window)
     per_head = [max_rel_err(got["O"][h], want[h]) for h in range(NH)]
-    # the floored relative form, printed so that a regression on small outputs shows even where
-    # the reference's metric (closer to an absolute bound near zero) still passes
-    g, e = np.asarray(got["O"], np.float64), want
-    floored = float(np.max(np.abs(g - e) / np.maximum(np.abs(e), 1e-3)))
+    floored = floored_rel_err(got["O"], want)
     print(exe.stage_kernel(2), window, f"max |g-e|/(1+|e|) {max(per_head):.3e}",
           f"max |g-e|/max(|e|,1e-3) {floored:.3e}")
     bad = [h for h, err in enumerate(per_head) if not err < 2e-2]
