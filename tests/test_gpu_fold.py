@@ -71,6 +71,27 @@ def test_split_fold_merges_in_last_workgroup(dev):
         assert int(out[0]) == 77_777
 
 
+@pytest.mark.parametrize("split", [1, 2, 3, 7, 9])
+def test_split_attention_equals_one_pass_for_any_block_count(dev, split):
+    """A 9-key attention fold split over 1, 2, 3, 7 and 9 workgroups (tests/group.rs:48-84:
+    2/3/7 leave uneven remainders, 9 puts one key in each workgroup so the last arriver's merge
+    does all of the softmax coupling) equals the one-pass oracle on the GPU."""
+    S, D = 9, 5
+    prog = configs.direct_attention(S=S, D=D, causal=False,
+                                    sched=Sched(lane_stream=True, waves=1, split=split))
+    vals = {n: oracle.lcg(seed, S * D).reshape(S, D) * 4.0 - 2.0 for n, seed in (("Q", 31), ("K", 32), ("V", 33))}
+    got, exe = run_on_gpu(dev, prog, vals)
+    if split > 1:
+        assert exe.stage_kernel(0).startswith("fold:split"), exe.stage_kernel(0)
+    want = oracle.run_program(prog, vals)["O"]
+    # the oracle's own split form agrees with its one pass (interp.rs:555-643)
+    split_want, _ = oracle.fold_stage(prog, 0, vals, blocks=split)
+    assert np.allclose(split_want, want, rtol=1e-6, atol=1e-7)
+    err = max_rel_err(got["O"], want)
+    print(exe.stage_kernel(0), split, err)
+    assert err < 1e-4
+
+
 def test_capture_feedback_converts_output_into_input(dev):
     """capture(bindings, feedback): a u32 output fed back into an f32 input inside the graph,
     so each replay sees the previous step's output (compile.rs:869-961, RunError::Feedback on
