@@ -390,9 +390,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // K rows: unpadded 128-byte rows with the 16-byte chunk index XORed by (row mod 8), like
     // the Q tile — a 72-element padded stride puts the 16 rows of one fragment read into 2-way
     // bank conflicts on gfx950 (measured: twice the LDS cycles of the swizzled form)
-    const bool kswz = true;
-    const int KS = 64;
-    k.line("__shared__ unsigned short k_lds[2][64 * " + std::to_string(KS) + "];");
+    k.line("__shared__ unsigned short k_lds[2][64 * 64];");
     k.line("__shared__ unsigned short v_lds[2][64 * " + std::to_string(VS) + "];");
     k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
     k.line("const int l16 = lane & 15, lq = lane >> 4;");
@@ -497,10 +495,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         c2.line("for (int u = 0; u < 2; ++u) {");
         c2.line("  const int ch = tid + u * 256;");
         c2.line("  const int r = ch >> 3, c8 = (ch & 7) * 8;");
-        if (kswz)
-            c2.line("  *(sanic_u32x4*)(&k_lds[" + buf + "][r * 64 + (c8 ^ ((r & 7) << 3))]) = kreg[u];");
-        else
-            c2.line("  *(sanic_u32x4*)(&k_lds[" + buf + "][r * " + std::to_string(KS) + " + c8]) = kreg[u];");
+        c2.line("  *(sanic_u32x4*)(&k_lds[" + buf + "][r * 64 + (c8 ^ ((r & 7) << 3))]) = kreg[u];");
         // V rows ([key][e]) or V^T rows ([e][key]) as they lie in memory
         c2.line("  *(sanic_u32x4*)(&v_lds[" + buf + "][r * " + std::to_string(VS) + " + c8]) = vreg[u];");
         c2.line("}");
@@ -539,10 +534,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("  s[kt][1] = (f32x4){0, 0, 0, 0};");
     k.line("  #pragma unroll");
     k.line("  for (int ds = 0; ds < 2; ++ds) {");
-    if (kswz)
-        k.line("    const bf16x8 ka = *(const bf16x8*)(&k_lds[buf][(kt * 16 + l16) * 64 + (((ds * 4 + lq) ^ (l16 & 7)) * 8)]);");
-    else
-        k.line("    const bf16x8 ka = *(const bf16x8*)(&k_lds[buf][(kt * 16 + l16) * " + std::to_string(KS) + " + ds * 32 + lq * 8]);");
+    k.line("    const bf16x8 ka = *(const bf16x8*)(&k_lds[buf][(kt * 16 + l16) * 64 + (((ds * 4 + lq) ^ (l16 & 7)) * 8)]);");
     k.line("    #pragma unroll");
     k.line("    for (int qt = 0; qt < 2; ++qt) {");
     k.line("      const int qr = wv * 32 + qt * 16 + l16;");

@@ -178,17 +178,13 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     const int WM = BM / WGM, WN = BN / 2;     // per-wave tile
     const int MT = WM / 16, NT = WN / 16;
     const int SR = (int)P.rslots.size();
-    int AS = 64 + 8;                          // LDS row strides (bf16)
-    int BS = 64 + 8;
-    // k-contiguous tiles: unpadded 128-byte rows with the 16-byte chunk index XORed by
-    // (row mod 8) — a 72-element padded stride 2-way bank-conflicts the 16-row operand reads
+    // k-contiguous tiles: unpadded 128-byte rows (64 bf16) with the 16-byte chunk index XORed
+    // by (row mod 8) — a 72-element padded stride 2-way bank-conflicts the 16-row operand reads
     // on gfx950
-    const bool kswz = true;
-    if (kswz) AS = BS = 64;
+    const int AS = 64, BS = 64;               // LDS row strides (bf16)
     // element offset of (row, k) in a k-contiguous tile; k a multiple of 8
-    auto koff = [&](const std::string& row, const std::string& k8, int stride) {
-        if (kswz) return "(" + row + ") * 64 + (((" + k8 + ") / 8) ^ ((" + row + ") & 7)) * 8";
-        return "(" + row + ") * " + std::to_string(stride) + " + " + k8;
+    auto koff = [&](const std::string& row, const std::string& k8, int) {
+        return "(" + row + ") * 64 + (((" + k8 + ") / 8) ^ ((" + row + ") & 7)) * 8";
     };
     // An operand that is not a bf16 input as stored (x·g, dequantized weights) goes to the MFMA
     // as hi + lo bf16 pair (hi = rn(v), lo = rn(v − hi): 16 significant bits, exact for the
