@@ -24,6 +24,8 @@ def _report(exe, got, want):
     (64, 256, 96, True),
     (192, 128, 160, False),
     (64, 512, 512, True),         # x·g built by the first launch (K % 512 == 0)
+    (128, 256, 16384, True),      # 8-wave 128 × 64 tiles, x·g built in-kernel (K % 512 != 0)
+    (256, 384, 8192, False),      # 8-wave tiles, [out, in] weights, in-kernel row slots
 ])
 def test_rmsnorm_gemm(dev, M, K, N, kmajor):
     prog = configs.rmsnorm_projection(M=M, K=K, N=N, kmajor=kmajor)
@@ -40,7 +42,7 @@ def test_rmsnorm_gemm(dev, M, K, N, kmajor):
     assert err < 2e-2
 
 
-@pytest.mark.parametrize("M,K,N,G", [(128, 2048, 8192, 64), (64, 512, 256, 32)])
+@pytest.mark.parametrize("M,K,N,G", [(128, 2048, 8192, 64), (64, 512, 256, 32), (256, 512, 8192, 64)])
 def test_int4_gemm(dev, M, K, N, G):
     """Config D2: packed uint4 [N, K], per-group scale and zero point, w = u·s − z."""
     prog = configs.int4_matmul(M=M, K=K, N=N, G=G)
