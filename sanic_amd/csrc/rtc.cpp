@@ -13,6 +13,7 @@
 #include <fstream>
 #include <mutex>
 #include <sstream>
+#include <vector>
 
 #include "common.h"
 
@@ -50,8 +51,17 @@ static bool read_file(const std::string& path, std::string& out) {
 }
 
 std::string compile_source(const std::string& generated) {
+    std::vector<std::string> opts(std::begin(kOptions), std::end(kOptions));
+    // a generated source may open with "// sched-strategy: <name>\n" to pick the machine
+    // scheduler's strategy for its kernel (set by the lowering that measured it faster)
+    static const std::string kMark = "// sched-strategy: ";
+    if (generated.compare(0, kMark.size(), kMark) == 0) {
+        const size_t eol = generated.find('\n');
+        opts.push_back("-mllvm");
+        opts.push_back("-amdgpu-sched-strategy=" + generated.substr(kMark.size(), eol - kMark.size()));
+    }
     std::string opts_key;
-    for (auto* o : kOptions) opts_key += o, opts_key += ' ';
+    for (auto& o : opts) opts_key += o, opts_key += ' ';
     char hex[32];
     snprintf(hex, sizeof hex, "%016llx", (unsigned long long)fnv1a(opts_key + generated));
     // debugging: SANIC_HIP_DUMP=<dir> writes every generated source as <dir>/<hash>.hip
@@ -78,7 +88,9 @@ std::string compile_source(const std::string& generated) {
     }
     if (cr != HIPRTC_SUCCESS)
         fail(SANIC_ERR_COMPILE, std::string("hiprtcCreateProgram failed: ") + hiprtcGetErrorString(cr));
-    hiprtcResult r = hiprtcCompileProgram(prog, (int)(sizeof kOptions / sizeof *kOptions), kOptions);
+    std::vector<const char*> optp;
+    for (auto& o : opts) optp.push_back(o.c_str());
+    hiprtcResult r = hiprtcCompileProgram(prog, (int)optp.size(), optp.data());
     if (r != HIPRTC_SUCCESS) {
         size_t n = 0;
         hiprtcGetProgramLogSize(prog, &n);

@@ -896,7 +896,9 @@ bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     src << kPrelude << R.args_struct({"float* __restrict__ scratch"});
     src << "extern \"C\" __global__ void __launch_bounds__(" << NT << ") " << kpart << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     out.kernel_kind = "skeleton:attn_decode[rep " + std::to_string(REP) + "]" + (writes.empty() ? "" : "+writes" + std::to_string(writes.size())) + (sep ? "+rowwg" : "");
-    out.source = src.str();
+    // the ILP-maximising machine scheduler: C3 11.2 → 10.75 µs (the default strategy interleaves
+    // the chunk's loads with its arithmetic to save registers)
+    out.source = "// sched-strategy: iterative-ilp\n" + src.str();
     out.variants = nvar;
     std::vector<Arg> args = R.arg_list();
     args.push_back({Arg::SCRATCH, sbase});

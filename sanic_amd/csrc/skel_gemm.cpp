@@ -717,7 +717,9 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     if (pre) src << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "_pre(Args a) {\n" << R.entry() << kp.str() << "}\n";
     src << "extern \"C\" __global__ void __launch_bounds__(" << NTH << ") " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     out.kernel_kind = "skeleton:gemm[" + std::to_string(BM) + "x" + std::to_string(BN) + (splitA ? ",a2" : "") + (splitB ? ",b2" : "") + (bkn ? ",kn" : "") + (pre ? ",pre" : "") + "]";
-    out.source = src.str();
+    // dequantized-weight tiles (int4): the ILP-maximising machine scheduler, D2 25.1 → 22.9 µs;
+    // bf16 tiles keep the default strategy (no measurable difference)
+    out.source = (splitB ? std::string("// sched-strategy: iterative-ilp\n") : std::string()) + src.str();
     std::vector<Arg> args = R.arg_list();
     if (pre) {
         args.push_back({Arg::SCRATCH, 0});
