@@ -958,7 +958,9 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         LoweredStage L;
         L.kernel_kind = "skeleton:gemv" + std::string(group.size() > 1 ? "[batched " + std::to_string(group.size()) + "]" : "") +
                         (paired >= 0 ? "+paired" : "") + (tails.empty() ? "" : "+tail" + std::to_string(tails.size()));
-        L.source = src.str();
+        // the memory-clause machine scheduler keeps the weight loads together: decode step
+        // 652.5 → 648.5 µs (three runs each)
+        L.source = "// sched-strategy: max-memory-clause\n" + src.str();
         L.variants = nvar;
         std::vector<Arg> args = R.arg_list();
         if (!tails.empty()) args.push_back({Arg::SCRATCH, counter_off});   // the tail counter: relative offset 0
@@ -1381,7 +1383,7 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         src << kPrelude << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(" << NT << ") " << kname << "(Args a) {\n"
             << R.entry() << k.str() << "}\n";
         out.kernel_kind = "skeleton:gemv_kmajor[strips " + std::to_string(SW) + "]";
-        out.source = src.str();
+        out.source = "// sched-strategy: max-memory-clause\n" + src.str();   // B1 12.26 → 12.07 µs
         out.launches.push_back({kname, "", dim3((unsigned)NS), dim3((unsigned)NT), 0, R.arg_list()});
         return true;
     }
