@@ -70,6 +70,27 @@ def test_lowering_chooses_the_expected_kernel(name):
     assert "extern \"C\" __global__" in src
 
 
+@pytest.mark.parametrize("name,prog,stage,strategy", [
+    ("C3", lambda: configs.decode_attention(), 0, "iterative-ilp"),
+    ("D2", lambda: configs.int4_matmul(M=128), 0, "iterative-ilp"),
+    ("B1", lambda: configs.rmsnorm_projection(kmajor=True), 0, "max-memory-clause"),
+    ("B1_rows", lambda: configs.rmsnorm_projection(kmajor=False), 0, "max-memory-clause"),
+    ("E_gateup", lambda: configs.llama_decode(), 8, "max-memory-clause"),
+    ("B2", lambda: configs.rmsnorm_projection(M=512), 0, None),
+    ("C1", lambda: configs.flash_prefill(), 2, None),
+    ("A", lambda: configs.direct_attention(), 0, None),
+])
+def test_kernels_carry_their_scheduler_strategy(name, prog, stage, strategy):
+    """The lowering marks the kernels measured faster under another machine-scheduler strategy
+    with a first source line the compiler step turns into `-amdgpu-sched-strategy=<name>`."""
+    kind, src = prog().emit(stage)
+    first = src.split("\n", 1)[0]
+    if strategy is None:
+        assert not first.startswith("// sched-strategy:"), (kind, first)
+    else:
+        assert first == "// sched-strategy: " + strategy, (kind, first)
+
+
 def test_precompile_small_program():
     configs.direct_attention(S=16, D=8).precompile()
 
