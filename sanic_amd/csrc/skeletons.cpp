@@ -959,8 +959,9 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         L.kernel_kind = "skeleton:gemv" + std::string(group.size() > 1 ? "[batched " + std::to_string(group.size()) + "]" : "") +
                         (paired >= 0 ? "+paired" : "") + (tails.empty() ? "" : "+tail" + std::to_string(tails.size()));
         // the memory-clause machine scheduler keeps the weight loads together: decode step
-        // 652.5 → 648.5 µs (three runs each)
-        L.source = "// sched-strategy: max-memory-clause\n" + src.str();
+        // 652.5 → 648.5 µs (three runs each); packed 4-bit weights, whose nibble decoding adds
+        // arithmetic per load, prefer the ILP form (D1 5.17 → 5.0 µs)
+        L.source = std::string(packed4 ? "// sched-strategy: iterative-ilp\n" : "// sched-strategy: max-memory-clause\n") + src.str();
         L.variants = nvar;
         std::vector<Arg> args = R.arg_list();
         if (!tails.empty()) args.push_back({Arg::SCRATCH, counter_off});   // the tail counter: relative offset 0

@@ -73,6 +73,7 @@ def test_lowering_chooses_the_expected_kernel(name):
 @pytest.mark.parametrize("name,prog,stage,strategy", [
     ("C3", lambda: configs.decode_attention(), 0, "iterative-ilp"),
     ("D2", lambda: configs.int4_matmul(M=128), 0, "iterative-ilp"),
+    ("D1", lambda: configs.int4_matmul(), 0, "iterative-ilp"),
     ("B1", lambda: configs.rmsnorm_projection(kmajor=True), 0, "max-memory-clause"),
     ("B1_rows", lambda: configs.rmsnorm_projection(kmajor=False), 0, "max-memory-clause"),
     ("E_gateup", lambda: configs.llama_decode(), 8, "max-memory-clause"),
