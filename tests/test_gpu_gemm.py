@@ -26,6 +26,7 @@ def _report(exe, got, want):
     (64, 512, 512, True),         # x·g built by the first launch (K % 512 == 0)
     (128, 256, 16384, True),      # 8-wave 128 × 64 tiles, x·g built in-kernel (K % 512 != 0)
     (256, 384, 8192, False),      # 8-wave tiles, [out, in] weights, in-kernel row slots
+    (128, 1536, 2048, True),      # operand-building launch with 3 k chunks over 4 waves
 ])
 def test_rmsnorm_gemm(dev, M, K, N, kmajor):
     prog = configs.rmsnorm_projection(M=M, K=K, N=N, kmajor=kmajor)
