@@ -958,10 +958,14 @@ bool lower_gemv_group(const sanic_program_desc* d, int si, int64_t& scratch, std
         LoweredStage L;
         L.kernel_kind = "skeleton:gemv" + std::string(group.size() > 1 ? "[batched " + std::to_string(group.size()) + "]" : "") +
                         (paired >= 0 ? "+paired" : "") + (tails.empty() ? "" : "+tail" + std::to_string(tails.size()));
-        // the memory-clause machine scheduler keeps the weight loads together: decode step
-        // 652.5 → 648.5 µs (three runs each); packed 4-bit weights, whose nibble decoding adds
-        // arithmetic per load, prefer the ILP form (D1 5.17 → 5.0 µs)
-        L.source = std::string(packed4 ? "// sched-strategy: iterative-ilp\n" : "// sched-strategy: max-memory-clause\n") + src.str();
+        // machine-scheduler strategy by shape (decode-step means of five runs each): the
+        // memory-clause form keeps the weight loads of large GEMVs together (gate/up, lm_head:
+        // 652.5 → 648.5 µs); long rows (K ≥ 4096, the down projection) and packed 4-bit weights,
+        // whose nibble decoding adds arithmetic per load, prefer the ILP form (648.6 → 646.9 µs
+        // together with the next rule; D1 5.17 → 5.0 µs); small GEMVs (≤ 8 Mi weights: q/k/v, o)
+        // keep the default
+        const char* strat = packed4 || K >= 4096 ? "iterative-ilp" : NTOT * K <= (int64_t(8) << 20) ? nullptr : "max-memory-clause";
+        L.source = (strat ? std::string("// sched-strategy: ") + strat + "\n" : std::string()) + src.str();
         L.variants = nvar;
         std::vector<Arg> args = R.arg_list();
         if (!tails.empty()) args.push_back({Arg::SCRATCH, counter_off});   // the tail counter: relative offset 0

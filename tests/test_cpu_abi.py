@@ -77,6 +77,10 @@ def test_lowering_chooses_the_expected_kernel(name):
     ("B1", lambda: configs.rmsnorm_projection(kmajor=True), 0, "max-memory-clause"),
     ("B1_rows", lambda: configs.rmsnorm_projection(kmajor=False), 0, "max-memory-clause"),
     ("E_gateup", lambda: configs.llama_decode(), 8, "max-memory-clause"),
+    ("E_down", lambda: configs.llama_decode(), 11, "iterative-ilp"),
+    ("E_o", lambda: configs.llama_decode(), 7, None),
+    ("E_qkv", lambda: configs.llama_decode(), 1, None),
+    ("E_lm_head", lambda: configs.llama_decode(), 177, "max-memory-clause"),
     ("B2", lambda: configs.rmsnorm_projection(M=512), 0, None),
     ("C1", lambda: configs.flash_prefill(), 2, None),
     ("A", lambda: configs.direct_attention(), 0, None),
