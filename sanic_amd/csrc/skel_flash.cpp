@@ -525,28 +525,40 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("const int full = __builtin_amdgcn_readfirstlane((int)(t0 >= flo && t0 + 64 <= fhi));");  // every row sees all
     // S^T tiles: kt (16 keys) × qt (16 queries), contraction over d in 2 steps of 32
     // both query tiles' scores first: each K fragment is read from LDS once for the two tiles
-    // (measured: 2% over re-reading it per tile, the kernel being bound by LDS and MFMA issue)
+    // (measured: 2% over re-reading it per tile, the kernel being bound by LDS and MFMA issue).
+    // The split variant and the rendered-mask reference variant keep one query tile's scores
+    // live at a time (with both live they spill 12–13 registers); the products are the same
+    // MFMAs in the same order either way.
+    const bool s_both = SPL == 1 && fvar != 3;
     k.line("f32x4 s[4][2];");
     k.line("sanic_u32x4 pw[2][2];");
-    k.line("#pragma unroll");
-    k.line("for (int kt = 0; kt < 4; ++kt) {");
-    k.line("  s[kt][0] = (f32x4){0, 0, 0, 0};");
-    k.line("  s[kt][1] = (f32x4){0, 0, 0, 0};");
-    k.line("  #pragma unroll");
-    k.line("  for (int ds = 0; ds < 2; ++ds) {");
-    k.line("    const bf16x8 ka = *(const bf16x8*)(&k_lds[buf][(kt * 16 + l16) * 64 + (((ds * 4 + lq) ^ (l16 & 7)) * 8)]);");
-    k.line("    #pragma unroll");
-    k.line("    for (int qt = 0; qt < 2; ++qt) {");
-    k.line("      const int qr = wv * 32 + qt * 16 + l16;");
-    k.line("      const bf16x8 qv = *(const bf16x8*)(&q_lds[qr * 64 + (((ds * 4 + lq) ^ (qr & 7)) * 8)]);");
-    k.line("      s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qv, s[kt][qt], 0, 0, 0);");
-    k.line("    }");
-    k.line("  }");
-    k.line("}");
+    auto scores = [&](bool both) {
+        k.line("#pragma unroll");
+        k.line("for (int kt = 0; kt < 4; ++kt) {");
+        k.line(both ? "  s[kt][0] = (f32x4){0, 0, 0, 0};" : "  s[kt][qt] = (f32x4){0, 0, 0, 0};");
+        if (both) k.line("  s[kt][1] = (f32x4){0, 0, 0, 0};");
+        k.line("  #pragma unroll");
+        k.line("  for (int ds = 0; ds < 2; ++ds) {");
+        k.line("    const bf16x8 ka = *(const bf16x8*)(&k_lds[buf][(kt * 16 + l16) * 64 + (((ds * 4 + lq) ^ (l16 & 7)) * 8)]);");
+        if (both) {
+            k.line("    #pragma unroll");
+            k.line("    for (int qt = 0; qt < 2; ++qt) {");
+        } else {
+            k.line("    {");
+        }
+        k.line("      const int qr = wv * 32 + qt * 16 + l16;");
+        k.line("      const bf16x8 qv = *(const bf16x8*)(&q_lds[qr * 64 + (((ds * 4 + lq) ^ (qr & 7)) * 8)]);");
+        k.line("      s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qv, s[kt][qt], 0, 0, 0);");
+        k.line("    }");
+        k.line("  }");
+        k.line("}");
+    };
+    if (s_both) scores(true);
     // online softmax per query column (lane-local; the max reduces across the 4 lane groups)
     k.line("#pragma unroll");
     k.line("for (int qt = 0; qt < 2; ++qt) {");
     k.indent++;
+    if (!s_both) scores(false);
     k.line("const int qi = (int)(q0 + qt * 16 + l16);");
     k.line("const int kb = (int)t0 + lq * 4;");
     k.line("float sv[16];");
