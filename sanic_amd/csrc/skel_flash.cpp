@@ -573,6 +573,21 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         k.line("const float mc = hmax3(s[1][qt][2], s[1][qt][3], s[2][qt][0]), md = hmax3(s[2][qt][1], s[2][qt][2], s[2][qt][3]);");
         k.line("const float me = hmax3(s[3][qt][0], s[3][qt][1], s[3][qt][2]);");
         k.line("float mt = hmax3(hmax3(ma, mb_, mc), hmax3(md, me, s[3][qt][3]), ma);");
+        // Common case: no lane's scores move its row's running max (every lane's own maximum
+        // within the rescale threshold, the running max finite). Then mn = m_run and alpha = 1
+        // exactly, as the general form below would find, without the cross-lane reduction,
+        // the rescale factor's exp2 or the rescale.
+        const std::string keep = lazy ? "m_run[qt] + " + flit(TAU) : std::string("m_run[qt]");
+        k.line("if (__all(mt * " + flit(scale_c) + " <= " + keep + " && m_run[qt] > -1e29f)) {");
+        k.line("  mn = m_run[qt];");
+        k.line("  alpha = 1.0f;");
+        k.line("  const float mb = mn * " + flit(LOG2E) + ";");
+        k.line("  #pragma unroll");
+        k.line("  for (int kt = 0; kt < 4; ++kt)");
+        k.line("    #pragma unroll");
+        k.line("    for (int r = 0; r < 4; ++r) p[kt * 4 + r] = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][r], " + flit(scale_c * LOG2E) + ", -mb));");
+        k.line("} else {");
+        k.indent++;
         k.line("mt = wave_max_x4(mt) * " + flit(scale_c) + ";");
         k.line(lazy ? "mn = mt > m_run[qt] + " + flit(TAU) + " ? mt : m_run[qt];" : "mn = fmaxf(m_run[qt], mt);");
         k.line("alpha = m_run[qt] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((m_run[qt] - mn) * " + flit(LOG2E) + ");");
@@ -587,6 +602,8 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         k.line("  for (int kt = 0; kt < 4; ++kt)");
         k.line("    #pragma unroll");
         k.line("    for (int r = 0; r < 4; ++r) p[kt * 4 + r] = mn == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f((s[kt][qt][r] * " + flit(scale_c) + " - mn) * " + flit(LOG2E) + ");");
+        k.line("}");
+        k.indent--;
         k.line("}");
         k.indent--;
         k.line("} else {");
