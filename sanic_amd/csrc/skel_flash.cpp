@@ -15,7 +15,8 @@
 //   the O rescale are lane-local, with one 4-lane shuffle per tile for the max);
 //   O^T += V^T·P^T with P packed to bf16 in registers (the MFMA k-order is chosen to match the
 //   S^T accumulator layout, so P never goes through LDS);
-//   K and V^T tiles are double-buffered in LDS; exp2 with log2(e) folded; the −∞ guard of the
+//   K and V tiles go from global memory straight into a ring of three LDS buffers, two tiles
+//   ahead; Q stays in registers; exp2 with log2(e) folded; the −∞ guard of the
 //   carrier's combine on the rescale; tiles outside every row's honest window are skipped and
 //   tiles entirely inside it skip the mask arithmetic;
 //   blockIdx → (KV head, query head, query block) places all query heads of one KV head on one
@@ -386,12 +387,12 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     const std::string kname = "sanic_flash_h" + std::to_string(NH) + "_s" + std::to_string(NQ) + "_t" + std::to_string(T);
     Code k;
     k.indent = 1;
-    const int VS = 72;   // LDS row stride (bf16) of the V tile: 64 + 8 padding
-    // K rows: unpadded 128-byte rows with the 16-byte chunk index XORed by (row mod 8), like
-    // the Q tile — a 72-element padded stride puts the 16 rows of one fragment read into 2-way
-    // bank conflicts on gfx950 (measured: twice the LDS cycles of the swizzled form)
-    k.line("__shared__ unsigned short k_lds[2][64 * 64];");
-    k.line("__shared__ unsigned short v_lds[2][64 * " + std::to_string(VS) + "];");
+    // K and V tiles in a ring of three LDS buffers, filled straight from global memory
+    // (global_load_lds, no register staging) two tiles ahead of the MFMAs. Rows are 128 bytes
+    // unpadded with the 16-byte chunk index XORed by (row mod 8): a padded stride would put the
+    // 16 rows of one fragment read into 2-way bank conflicts on gfx950, and the direct loads
+    // write each wave's 1 KB contiguously, so the swizzle is applied to the source addresses.
+    k.line("__shared__ __attribute__((aligned(16))) unsigned short kv_lds[3][2][64 * 64];");
     k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
     k.line("const int l16 = lane & 15, lq = lane >> 4;");
     // XCD-aware block order: blockIdx mod 8 picks the KV head group, heaviest query blocks first
@@ -444,15 +445,14 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // is tested against bit for bit)
     const bool edge_on = raw_ok && fvar != 3;
     // Q^T as the B operand (lane = query column l16 (+16·qt), d-slots lq·8 + 0..7 (+32·ds)),
-    // read from LDS each tile rather than held in registers: the block's 128 query rows, 16-byte
-    // chunks XOR-swizzled by row so the 16 rows a lane group reads hit different banks
-    k.line("__shared__ __attribute__((aligned(16))) unsigned short q_lds[128 * 64];");
+    // held in registers for the whole key loop, loaded once from global memory
+    k.line("bf16x8 qf[2][2];");
     k.line("#pragma unroll");
-    k.line("for (int u = 0; u < 4; ++u) {");
-    k.line("  const int ch = tid + u * 256, r = ch >> 3, cc = ch & 7;");
-    k.line("  *(sanic_u32x4*)(&q_lds[r * 64 + ((cc ^ (r & 7)) * 8)]) = *(const sanic_u32x4*)(" + qp + " + " + std::to_string(P.qacc.addr.c0) + " + " +
-           hterm(qc, qh, qhc) + " + (qb * 128 + r) * " + std::to_string(qc[3]) + " + cc * 8);");
-    k.line("}");
+    k.line("for (int qt = 0; qt < 2; ++qt)");
+    k.line("  #pragma unroll");
+    k.line("  for (int ds = 0; ds < 2; ++ds)");
+    k.line("    qf[qt][ds] = *(const bf16x8*)(" + qp + " + " + std::to_string(P.qacc.addr.c0) + " + " + hterm(qc, qh, qhc) +
+           " + (q0 + qt * 16 + l16) * " + std::to_string(qc[3]) + " + (ds * 4 + lq) * 8);");
     k.line("f32x4 o[4][2];");
     k.line("#pragma unroll");
     k.line("for (int dt = 0; dt < 4; ++dt) { o[dt][0] = (f32x4){0, 0, 0, 0}; o[dt][1] = (f32x4){0, 0, 0, 0}; }");
@@ -474,50 +474,38 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     };
     const bool lazy = !reads_f(c.project);
     const double TAU = 8.0 / LOG2E;
-    // cooperative tile loads: K tile (64 keys × 64 d) and V tile, 2 × 16 B per thread each
+    // One tile (K: 64 keys × 64 d; V rows [key][e] or V^T rows [e][key] as they lie in memory)
+    // into ring buffer b: wave w's transfer u fills LDS rows 8(w + 4u) .. +7, lane l landing on
+    // row 8(w + 4u) + l/8, chunk l%8 — so it fetches global chunk (l%8) ^ (l/8) of that row.
+    // Four transfers per lane per tile, counted by vmcnt like any global load.
     std::string kbase = std::to_string(P.kacc.addr.c0) + " + " + hterm(kc, kh, khc);
     std::string vbase = std::to_string(P.vacc.addr.c0) + " + " + hterm(vc, vh, vhc);
-    k.line("sanic_u32x4 kreg[2], vreg[2];");
-    auto load_tile = [&](Code& c2, const std::string& t0) {
-        c2.line("#pragma unroll");
-        c2.line("for (int u = 0; u < 2; ++u) {");
-        c2.line("  const int ch = tid + u * 256;");           // 512 chunks of 8 bf16
-        c2.line("  const int r = ch >> 3, c8 = (ch & 7) * 8;");
-        c2.line("  kreg[u] = *(const sanic_u32x4*)(" + kp + " + " + kbase + " + (" + t0 + " + r) * " + std::to_string(kc[1]) + " + c8);");
-        if (v_rows)
-            c2.line("  vreg[u] = *(const sanic_u32x4*)(" + vp + " + " + vbase + " + (" + t0 + " + r) * " + std::to_string(vc[1]) + " + c8);");
-        else   // V^T in memory: row = e, 8 consecutive keys
-            c2.line("  vreg[u] = *(const sanic_u32x4*)(" + vp + " + " + vbase + " + (idx_t)r * " + std::to_string(vc[2]) + " + " + t0 + " + c8);");
-        c2.line("}");
-    };
-    auto store_tile = [&](Code& c2, const std::string& buf) {
-        c2.line("#pragma unroll");
-        c2.line("for (int u = 0; u < 2; ++u) {");
-        c2.line("  const int ch = tid + u * 256;");
-        c2.line("  const int r = ch >> 3, c8 = (ch & 7) * 8;");
-        c2.line("  *(sanic_u32x4*)(&k_lds[" + buf + "][r * 64 + (c8 ^ ((r & 7) << 3))]) = kreg[u];");
-        // V rows ([key][e]) or V^T rows ([e][key]) as they lie in memory
-        c2.line("  *(sanic_u32x4*)(&v_lds[" + buf + "][r * " + std::to_string(VS) + " + c8]) = vreg[u];");
-        c2.line("}");
-    };
+    k.line("auto fetch = [&](idx_t tt, int b) {");
+    k.line("  #pragma unroll");
+    k.line("  for (int u = 0; u < 2; ++u) {");
+    k.line("    const int r = 8 * (wv + 4 * u) + (lane >> 3), c = (lane & 7) ^ (lane >> 3);");
+    k.line("    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(" + kp + " + " + kbase + " + (tt + r) * " +
+           std::to_string(kc[1]) + " + c * 8), (__attribute__((address_space(3))) void*)(&kv_lds[b][0][(wv + 4 * u) * 512]), 16, 0, 0);");
+    const std::string vsrc = v_rows ? "(tt + r) * " + std::to_string(vc[1]) + " + c * 8"
+                                    : "(idx_t)r * " + std::to_string(vc[2]) + " + tt + c * 8";
+    k.line("    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(" + vp + " + " + vbase + " + " + vsrc +
+           "), (__attribute__((address_space(3))) void*)(&kv_lds[b][1][(wv + 4 * u) * 512]), 16, 0, 0);");
+    k.line("  }");
+    k.line("};");
     k.line("if (klo < khi) {");
     k.indent++;
-    load_tile(k, "klo");
-    store_tile(k, "0");
-    k.line("__syncthreads();");
-    // every load issued so far (the Q fragments, the first tile) has landed: without this the
-    // loop's first MFMA carries a conservative vmcnt wait that, in every later iteration, stalls
-    // on the next tile's prefetch
-    k.line("__builtin_amdgcn_s_waitcnt(0);");
+    k.line("fetch(klo, 0);");
+    k.line("if (klo + 64 < khi) fetch(klo + 64, 1);");
     k.line("int buf = 0;");
     k.line("for (idx_t t0 = klo; t0 < khi; t0 += 64) {");
     k.indent++;
-    k.line("const bool more = t0 + 64 < khi;");
-    k.line("if (more) {");
-    k.indent++;
-    load_tile(k, "(t0 + 64)");
-    k.indent--;
-    k.line("}");
+    // this tile's transfers have landed for every wave (only the next tile's four may still be
+    // in flight; loads complete in issue order), and every wave is done reading the buffer the
+    // transfer below refills (read two tiles ago). The asm carries the memory clobber that keeps
+    // the compiler from moving LDS accesses across the barrier.
+    k.line("if (t0 + 64 < khi) asm volatile(\"s_waitcnt vmcnt(4)\\n\\ts_barrier\" ::: \"memory\");");
+    k.line("else asm volatile(\"s_waitcnt vmcnt(0)\\n\\ts_barrier\" ::: \"memory\");");
+    k.line("if (t0 + 128 < khi) fetch(t0 + 128, buf == 0 ? 2 : buf - 1);");
     // wave-uniform tile classification (scalar branches)
     k.line("const int live = __builtin_amdgcn_readfirstlane((int)(t0 < whi && t0 + 64 > wlo));");   // some row sees it
     k.line("if (live) {");
@@ -539,16 +527,14 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         if (both) k.line("  s[kt][1] = (f32x4){0, 0, 0, 0};");
         k.line("  #pragma unroll");
         k.line("  for (int ds = 0; ds < 2; ++ds) {");
-        k.line("    const bf16x8 ka = *(const bf16x8*)(&k_lds[buf][(kt * 16 + l16) * 64 + (((ds * 4 + lq) ^ (l16 & 7)) * 8)]);");
+        k.line("    const bf16x8 ka = *(const bf16x8*)(&kv_lds[buf][0][(kt * 16 + l16) * 64 + (((ds * 4 + lq) ^ (l16 & 7)) * 8)]);");
         if (both) {
             k.line("    #pragma unroll");
             k.line("    for (int qt = 0; qt < 2; ++qt) {");
         } else {
             k.line("    {");
         }
-        k.line("      const int qr = wv * 32 + qt * 16 + l16;");
-        k.line("      const bf16x8 qv = *(const bf16x8*)(&q_lds[qr * 64 + (((ds * 4 + lq) ^ (qr & 7)) * 8)]);");
-        k.line("      s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qv, s[kt][qt], 0, 0, 0);");
+        k.line("      s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[qt][ds], s[kt][qt], 0, 0, 0);");
         k.line("    }");
         k.line("  }");
         k.line("}");
@@ -693,13 +679,17 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         // V rows in LDS, read transposed (ds_read_b64_tr_b16): in each 16-lane group, source
         // lane s reads 4 values of e at key row (base + s/4), e = dt·16 + 4·(s%4); lane i then
         // holds keys base + 0..3 of e = dt·16 + i — slots 0..3, and base + 16 gives slots 4..7
-        k.line("    const unsigned short* vr = &v_lds[buf][(ks * 32 + lq * 4 + (l16 >> 2)) * " + std::to_string(VS) + " + dt * 16 + (l16 & 3) * 4];");
+        // (row + 16 has the same swizzle as row)
+        k.line("    const int vrow = ks * 32 + lq * 4 + (l16 >> 2), vcol = dt * 16 + (l16 & 3) * 4;");
+        k.line("    const unsigned short* vr = &kv_lds[buf][1][vrow * 64 + (((vcol >> 3) ^ (vrow & 7)) << 3) + (vcol & 7)];");
         k.line("    const sanic_s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(vr));");
-        k.line("    const sanic_s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(vr + 16 * " + std::to_string(VS) + "));");
+        k.line("    const sanic_s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(vr + 16 * 64));");
         k.line("    const bf16x8 va = __builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));");
     } else {
-        k.line("    const unsigned short* vr = &v_lds[buf][(dt * 16 + l16) * " + std::to_string(VS) + " + ks * 32 + lq * 4];");
-        k.line("    const uint2 lo4 = *(const uint2*)(vr), hi4 = *(const uint2*)(vr + 16);");
+        k.line("    const int vrow = dt * 16 + l16, vcol = ks * 32 + lq * 4;");
+        k.line("    const unsigned short* vr = &kv_lds[buf][1][vrow * 64 + (((vcol >> 3) ^ (vrow & 7)) << 3) + (vcol & 7)];");
+        k.line("    const unsigned short* vr2 = &kv_lds[buf][1][vrow * 64 + ((((vcol + 16) >> 3) ^ (vrow & 7)) << 3) + (vcol & 7)];");
+        k.line("    const uint2 lo4 = *(const uint2*)(vr), hi4 = *(const uint2*)(vr2);");
         k.line("    const bf16x8 va = __builtin_bit_cast(bf16x8, (sanic_u32x4){lo4.x, lo4.y, hi4.x, hi4.y});");
     }
     k.line("    o[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[0][ks], o[dt][0], 0, 0, 0);");
@@ -707,13 +697,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("  }");
     k.indent--;
     k.line("}");
-    k.line("if (more) {");
-    k.indent++;
-    store_tile(k, "buf ^ 1");
-    k.indent--;
-    k.line("}");
-    k.line("__syncthreads();");
-    k.line("buf ^= 1;");
+    k.line("buf = buf == 2 ? 0 : buf + 1;");
     k.indent--;
     k.line("}");
     k.indent--;
