@@ -31,15 +31,17 @@ def direct_attention(S: int = 128, D: int = 64, causal: bool = True, dtype: int 
 
 
 def flash_prefill(NH: int = 32, NKV: int = 8, S: int = 4096, HD: int = 64, theta: float = 500000.0,
-                  window: int = 0, rope_stages: bool = True) -> Program:
+                  window: int = 0, rope_stages: bool = True, v_transposed: bool = False) -> Program:
     """Config C (prefill): GQA causal attention over S tokens, RoPE (rotate-half, plain
     inv_freq, each row at its own position) on Q and K, scale 1/√HD; `window` > 0 adds the
     sliding-window mask (key visible iff q − window + 1 ≤ k ≤ q). The RoPE'd Q and K are
-    materialised by two pointwise stages (bf16), then one FlashAttention carrier fold."""
+    materialised by two pointwise stages (bf16), then one FlashAttention carrier fold.
+    `v_transposed` stores V as [NKV, HD, S] (keys contiguous, the decode cache's layout) and
+    reads it through a transposed view."""
     p = Program()
     q = p.input("Q", (NH, S, HD), ir.BF16)
     k = p.input("K", (NKV, S, HD), ir.BF16)
-    v = p.input("V", (NKV, S, HD), ir.BF16)
+    v = ir.transpose(p.input("V", (NKV, HD, S), ir.BF16), 1, 2) if v_transposed else p.input("V", (NKV, S, HD), ir.BF16)
     if rope_stages:
         invf = ir.rope_inv_freq(theta, HD // 2)
         rows = ir.iota(S)

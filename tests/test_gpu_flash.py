@@ -63,3 +63,26 @@ def test_flash_full_size_all_heads(dev, window):
           f"max |g-e|/max(|e|,1e-3) {floored:.3e}")
     bad = [h for h, err in enumerate(per_head) if not err < 2e-2]
     assert not bad, [(h, per_head[h]) for h in bad]
+
+
+@pytest.mark.parametrize("S,window", [(256, 0), (384, 100)])
+def test_flash_transposed_values_layout(dev, S, window):
+    """V stored [NKV, HD, S] (keys contiguous, as in the decode cache) and read through a
+    transposed view: the skeleton loads those rows as they lie and reads its PV operand without
+    the transposing LDS read — against the oracle, and bit for bit against the same values
+    stored [NKV, S, HD] (the MFMAs see the same operands in the same order)."""
+    NH, NKV = 4, 2
+    vals = _inputs(NH, NKV, S, seed=430)
+    outs = []
+    for vt in (False, True):
+        prog = configs.flash_prefill(NH, NKV, S, window=window, rope_stages=False, v_transposed=vt)
+        v = {"Q": vals["Q"], "K": vals["K"], "V": vals["V"].transpose(0, 2, 1).copy() if vt else vals["V"]}
+        got, exe = run_on_gpu(dev, prog, v)
+        assert exe.stage_kernel(0).startswith("skeleton:flash_prefill"), exe.stage_kernel(0)
+        outs.append(got["O"])
+        if vt:
+            want = oracle.run_program(prog, v)["O"]
+            err = max_rel_err(got["O"], want)
+            print(S, window, err, floored_rel_err(got["O"], want))
+            assert err < 2e-2
+    assert np.array_equal(outs[0], outs[1])
