@@ -86,3 +86,18 @@ def test_flash_transposed_values_layout(dev, S, window):
             print(S, window, err, floored_rel_err(got["O"], want))
             assert err < 2e-2
     assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("NH,NKV", [(8, 8), (16, 2), (8, 1), (16, 16), (24, 8)])
+def test_flash_head_groupings(dev, NH, NKV):
+    """Query heads per KV head 1 (MHA), 8 and 3, and KV head counts on both sides of the
+    XCD-aware block order (a multiple of 8 or not): every head against the oracle."""
+    S = 256
+    prog = configs.flash_prefill(NH, NKV, S, rope_stages=False)
+    vals = _inputs(NH, NKV, S, seed=450 + NH + NKV)
+    got, exe = run_on_gpu(dev, prog, vals)
+    assert exe.stage_kernel(0).startswith("skeleton:flash_prefill"), exe.stage_kernel(0)
+    want = oracle.run_program(prog, vals)["O"]
+    err = max_rel_err(got["O"], want)
+    print(NH, NKV, err, floored_rel_err(got["O"], want))
+    assert err < 2e-2
