@@ -86,3 +86,18 @@ def test_flash_prefill_ragged(dev, S, window):
     want = oracle.run_program(prog, vals)["O"]
     print([exe.stage_kernel(i) for i in range(3)], max_rel_err(got["O"], want), floored_rel_err(got["O"], want))
     assert max_rel_err(got["O"], want) < 2e-2
+
+
+@pytest.mark.parametrize("NH,NKV", [(8, 8), (16, 2), (24, 8), (8, 1)])
+def test_decode_attention_head_groupings(dev, NH, NKV):
+    """Query heads per KV head 1, 8 and 3 (the workgroup holds all query heads of its KV
+    group): every head against the oracle, position past the first chunk."""
+    cap, pos = 640, 601
+    prog = configs.decode_attention(NH, NKV, 64, cap)
+    vals = _vals(prog, 900 + NH + NKV)
+    vals["position"] = np.array(float(pos))
+    got, exe = run_on_gpu(dev, prog, vals)
+    want = oracle.run_program(prog, vals)["o"]
+    print(exe.stage_kernel(0), NH, NKV, max_rel_err(got["o"], want), floored_rel_err(got["o"], want))
+    assert exe.stage_kernel(0).startswith("skeleton:attn_decode")
+    assert max_rel_err(got["o"], want) < 2e-2
