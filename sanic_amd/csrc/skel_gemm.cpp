@@ -206,6 +206,9 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             if (other && other->op == SANIC_EX_ITEM && raw_bf16_input(other->index)) splitA = false;
         }
     }
+    // A is one stored bf16 row leaf and no row slot reads it: its 16-byte runs go to LDS as
+    // loaded (no unpack to f32 and repack)
+    bool rawA = !splitA && P.rslots.empty() && P.rows.size() == 1;
 
     Renderer R(d);
     // weight leaf vector form over vars {0: n, 1: k}
@@ -255,6 +258,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         Code l1, d1;
         render_weight_run(d, st.leaf[l], cr, {M, K}, l1, d1, "mm", "k0", "_p", rb, rd, rok, rc, rr, false);
         if (!rok || !rc) return false;
+        if (rr.empty()) rawA = false;
         crow.push_back(cr);
     }
 
@@ -372,6 +376,11 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
                                               "_a" + std::to_string(li) + "_" + std::to_string(r) + sfx, rb, rd, rok, rc, rr, false);
                 for (size_t b = 0; b < rb.size(); b++)
                     c2.line("const " + std::string(ctype_of(rd[b])) + "* __restrict__ wb" + std::to_string(b) + "_a" + std::to_string(li) + "_" + std::to_string(r) + sfx + " = " + R.param(rb[b]) + ";");
+                if (rawA && !rr.empty()) {
+                    c2.s << l1.str();
+                    c2.line("const sanic_u32x4 rawa" + std::to_string(r) + sfx + " = " + rr + ";");
+                    continue;
+                }
                 c2.s << l1.str() << d1.str();
                 for (int j = 0; j < 8; j++)
                     c2.line("const float ra" + std::to_string(li) + "_" + std::to_string(r) + "_" + std::to_string(j) + sfx + " = " + vals[j] + ";");
@@ -430,7 +439,11 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             c2.line("*(sanic_u32x4*)(&a_lds[" + buf + "][" + aoff + "]) = pah" + rs + sfx + ";");
             c2.line("*(sanic_u32x4*)(&a_lo[" + buf + "][" + aoff + "]) = pal" + rs + sfx + ";");
         }
-        for (int r = 0; r < RUNS_A && !pre; r++) {
+        for (int r = 0; r < RUNS_A && !pre && rawA; r++) {
+            const std::string aoff = koff("ar", "(tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8), AS);
+            c2.line("*(sanic_u32x4*)(&a_lds[" + buf + "][" + aoff + "]) = rawa" + std::to_string(r) + sfx + ";");
+        }
+        for (int r = 0; r < RUNS_A && !pre && !rawA; r++) {
             std::string rs = std::to_string(r);
             // rest of the contraction slot (A) and the row slots, per element
             std::string pk[4];
