@@ -122,3 +122,17 @@ def test_unpadded_out_of_bounds_reindex_is_rejected():
     p.pointwise("Y", shifted, ir.F32)
     with pytest.raises(abi.SanicError):
         p.emit(0)
+
+
+def test_int4_gemv_folds_each_run_as_scale_and_zero():
+    """A packed 4-bit weight q·s − z with s, z constant over a run of 8 is folded per run
+    (s·Σx·q − z·Σx, no per-element dequantization) in the GEMV; a bf16 GEMV and the int4 GEMM
+    keep their per-element forms."""
+    kind, src = configs.int4_matmul(M=1).emit(0)
+    assert kind.startswith("skeleton:gemv")
+    assert "rr0_0 = fmaf(" in src and "xs_0 +=" in src and "0x0F0F0F0Fu" in src
+    assert "acc0_0 = fmaf(-" in src                       # the zero point enters once per run
+    kind, src = configs.rmsnorm_projection(M=1, kmajor=False).emit(0)
+    assert kind.startswith("skeleton:gemv") and "rr0_0" not in src
+    kind, src = configs.int4_matmul(M=128).emit(0)
+    assert kind.startswith("skeleton:gemm") and "0x0F0F0F0Fu" not in src
