@@ -101,3 +101,37 @@ def test_decode_attention_head_groupings(dev, NH, NKV):
     print(exe.stage_kernel(0), NH, NKV, max_rel_err(got["o"], want), floored_rel_err(got["o"], want))
     assert exe.stage_kernel(0).startswith("skeleton:attn_decode")
     assert max_rel_err(got["o"], want) < 2e-2
+
+
+def _int4_form(form, M=1, K=2048, N=512, G=64):
+    """y = x · dequant(W)ᵀ with the packed 4-bit weight written three ways: q·s − z (the
+    reference's grouped W4 graph), q·s (no zero point) and (q − z)·s (zero subtracted first)."""
+    from sanic_amd import carrier as C
+    from sanic_amd.program import STREAM, Program
+    p = Program()
+    x = p.input("x", (M, K), ir.BF16)
+    wq = p.input("Wq", (N, K // G, G), ir.U4)
+    s = ir.unsqueeze(p.input("S", (N, K // G), ir.BF16), 2)
+    z = ir.unsqueeze(p.input("Z", (N, K // G), ir.BF16), 2)
+    if form == "qs-z":
+        deq = ir.map_(ir.SUB, ir.map_(ir.MUL, wq, s), z)
+    elif form == "qs":
+        deq = ir.map_(ir.MUL, wq, s)
+    else:
+        deq = ir.map_(ir.MUL, ir.map_(ir.SUB, wq, z), s)
+    p.fused("y", (M, N), K, [(x, (0, STREAM)), (ir.flatten(deq, 1, 2), (1, STREAM))], C.dot(2), ir.F32)
+    return p
+
+
+@pytest.mark.parametrize("form", ["qs-z", "qs", "q-z_s"])
+def test_int4_gemv_dequant_forms(dev, form):
+    """The GEMV folds a run of 8 as s·Σx·q − z·Σx when the weight is q·s ± z or q·s, and
+    dequantizes per element otherwise; every form against the oracle at the f32 bound."""
+    prog = _int4_form(form)
+    vals = _vals(prog, 950)
+    got, exe = run_on_gpu(dev, prog, vals)
+    want = oracle.run_program(prog, vals)["y"]
+    err = max_rel_err(got["y"], want)
+    print(exe.stage_kernel(0), form, err)
+    assert exe.stage_kernel(0).startswith("skeleton:gemv")
+    assert err < 1e-4
