@@ -292,17 +292,24 @@ int sanic_hip_exe_stage_source(const sanic_hip_exe* exe, int stage, char* out, s
 int sanic_hip_execute(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int n_bindings,
                       sanic_hip_buffer** outputs);
 
-/* No counterpart in the reference. Backend::execute without allocation, for callers that cannot
- * call hipMalloc (code under HIP graph capture, tight serving loops, harnesses that forbid it):
+/* No counterpart in the reference. sanic_hip_execute without device allocation, for callers
+ * that cannot call hipMalloc (code under HIP graph capture, tight serving loops, harnesses that forbid it):
  * `bindings[i]` must hold a caller-owned buffer for every INPUT, STATE and OUTPUT program buffer
  * (NULL for SCRATCH-role ones). The executable's intermediates and its split-partial / counter
  * arena live in the library's static device scratch — 32 MiB per GPU, held until the process
  * ends; a program that needs more is refused with SANIC_ERR_ARG. The stages are enqueued on the
  * device's stream and the call returns without waiting (a download on the same buffers waits).
- * Every call on one GPU shares that scratch, so calls that overlap on one GPU race; the arena's
- * counters are cleared at the start of each call, its other contents are whatever the last call
- * left. In-place programs are refused as by sanic_hip_execute. */
+ * Every call on one GPU shares that scratch; the arena's counters are cleared at the start of
+ * each call, its other contents are whatever the last call left. Eager calls are ordered per GPU:
+ * each waits for the previous eager call's work on that GPU, whichever device handle (stream)
+ * made it. A call made while the device's stream is being captured into a HIP graph is not
+ * ordered that way: replays of such a graph that overlap other calls on the GPU race on the
+ * scratch. In-place programs are refused as by sanic_hip_execute. */
 int sanic_hip_execute_static(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int n_bindings);
+
+/* No counterpart in the reference. The number of device allocations (hipMalloc) this library
+ * has made in this process; a test hook showing that sanic_hip_execute_static allocates none. */
+uint64_t sanic_hip_device_allocations(void);
 
 /* Program::capture (compile.rs:820-961): freeze the bindings into a hipGraph of every stage.
  * feedback = n_pairs (output buffer index, input buffer index) pairs: after each step the

@@ -95,6 +95,7 @@ SIGNATURES = {
     "sanic_hip_exe_stage_source": (I, [VP, I, ctypes.c_char_p, SZ]),
     "sanic_hip_execute": (I, [VP, ctypes.POINTER(VP), I, ctypes.POINTER(VP)]),
     "sanic_hip_execute_static": (I, [VP, ctypes.POINTER(VP), I]),
+    "sanic_hip_device_allocations": (ctypes.c_uint64, []),
     "sanic_hip_capture": (I, [VP, ctypes.POINTER(VP), I, ctypes.POINTER(ctypes.c_int32), I,
                               ctypes.POINTER(VP)]),
     "sanic_hip_replay_buffer": (I, [VP, I, ctypes.POINTER(VP)]),

@@ -1040,7 +1040,7 @@ FoldChoice choose_fold_sched(const sanic_program_desc* d, const sanic_stage& st)
     for (int w : {1, 2, 4, 8, 16})
         for (int sp : {1, 2, 4, 8, 16, 32, 64}) {
             if (64.0 * w * sp > S) continue;            // an empty split unit would merge identity
-            if (sp > 1 && gvol * sp * c.slots * 4.0 > 64.0 * (1 << 20)) continue;   // partials stay ≤ 64 MB
+            if (sp > 1 && gvol * sp * c.slots * 4.0 > 16.0 * (1 << 20)) continue;   // partials stay ≤ 16 MiB (half of execute_static's scratch)
             const double t = price(w, sp, 1);
             if (t < best.time || (t == best.time && best.waves == 0)) best = {w, sp, 1, t};
         }

@@ -43,6 +43,13 @@ struct sanic_hip_device {
 static const size_t kStaticScratchBytes = size_t(32) << 20;
 static __device__ __align__(256) char scratch[kStaticScratchBytes];
 
+// One event per GPU marking the end of the last sanic_hip_execute_static call's work on that
+// GPU. Each call makes its stream wait on it before touching the scratch and records it after
+// enqueueing, so calls from different device handles (each with its own stream) on one GPU are
+// ordered instead of racing on the shared scratch. Created once per ordinal in sanic_hip_open.
+static std::mutex g_static_mu;
+static std::map<int, hipEvent_t> g_static_done;
+
 struct Storage {
     void* ptr = nullptr;
     size_t bytes = 0;
@@ -159,8 +166,12 @@ static int64_t buffer_bytes(const sanic_buffer_desc& b) {
     return dtype_bytes(b.dtype, n);
 }
 
+// device allocations made by this library (every one goes through new_buffer)
+static std::atomic<uint64_t> g_device_allocations{0};
+
 static sanic_hip_buffer* new_buffer(sanic_hip_device* dev, size_t bytes) {
     SANIC_HIP(hipSetDevice(dev->ordinal));
+    g_device_allocations.fetch_add(1, std::memory_order_relaxed);
     auto st = std::make_shared<Storage>();
     st->bytes = bytes;
     st->owned = true;
@@ -333,6 +344,19 @@ int sanic_hip_open(int ordinal, sanic_hip_device** out) {
             fail(SANIC_ERR_BACKEND, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(se));
         }
         d->scratch_ptr = (char*)sp;
+        {
+            std::lock_guard<std::mutex> lk(g_static_mu);
+            if (!g_static_done.count(ordinal)) {
+                hipEvent_t ev = nullptr;
+                hipError_t ee = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+                if (ee != hipSuccess) {
+                    hipStreamDestroy(d->stream);
+                    delete d;
+                    fail(SANIC_ERR_BACKEND, std::string("hipEventCreateWithFlags: ") + hipGetErrorString(ee));
+                }
+                g_static_done[ordinal] = ev;
+            }
+        }
         *out = d;
     });
 }
@@ -520,7 +544,7 @@ int sanic_hip_execute_static(sanic_hip_exe* exe, sanic_hip_buffer* const* bindin
         if (!exe || !bindings) fail(SANIC_ERR_ARG, "null argument");
         for (int r : exe->stage_out_role)
             if (r == SANIC_BUF_STATE)
-                fail(SANIC_ERR_IN_PLACE, "this program writes state in place; use capture (compile.rs:745-751)");
+                fail(SANIC_ERR_IN_PLACE, "this program writes state in place; use sanic_hip_capture");
         const int nb = (int)exe->buffers.size();
         if (n_bindings != nb) fail(SANIC_ERR_ARG, "expected " + std::to_string(nb) + " bindings, got " + std::to_string(n_bindings));
         char* base = exe->dev->scratch_ptr;
@@ -557,6 +581,18 @@ int sanic_hip_execute_static(sanic_hip_exe* exe, sanic_hip_buffer* const* bindin
         }
         SANIC_HIP(hipSetDevice(exe->dev->ordinal));
         hipStream_t s = exe->dev->stream;
+        hipEvent_t done;
+        {
+            std::lock_guard<std::mutex> lk(g_static_mu);
+            done = g_static_done.at(exe->dev->ordinal);
+        }
+        // after the previous call's work on this GPU, whichever stream it ran on (a wait on a
+        // never-recorded event is satisfied at once); not under graph capture, where an event
+        // recorded outside the graph is no dependency the graph can hold
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        SANIC_HIP(hipStreamIsCapturing(s, &cap));
+        const bool eager = cap == hipStreamCaptureStatusNone;
+        if (eager) SANIC_HIP(hipStreamWaitEvent(s, done, 0));
         // arrival counters start at zero (a fill kernel, not a memset: safe under graph capture)
         if (arena > 0) {
             const int64_t words = arena / 4;
@@ -565,8 +601,11 @@ int sanic_hip_execute_static(sanic_hip_exe* exe, sanic_hip_buffer* const* bindin
             SANIC_HIP(hipGetLastError());
         }
         enqueue(exe, bound, base);
+        if (eager) SANIC_HIP(hipEventRecord(done, s));
     });
 }
+
+uint64_t sanic_hip_device_allocations(void) { return g_device_allocations.load(std::memory_order_relaxed); }
 
 int sanic_hip_capture(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int n_bindings, const int32_t* feedback,
                       int n_pairs, sanic_hip_replay** out) {

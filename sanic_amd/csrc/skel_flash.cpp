@@ -500,8 +500,9 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("for (idx_t t0 = klo; t0 < khi; t0 += 64) {");
     k.indent++;
     // this tile's transfers have landed for every wave (only the next tile's four may still be
-    // in flight; loads complete in issue order), and every wave is done reading the buffer the
-    // transfer below refills (read two tiles ago). The asm carries the memory clobber that keeps
+    // in flight; loads complete in issue order). The buffer the transfer below refills was read
+    // in the previous iteration: this barrier orders every wave's reads of it before the refill,
+    // so the refill must stay after the barrier. The asm carries the memory clobber that keeps
     // the compiler from moving LDS accesses across the barrier.
     k.line("if (t0 + 64 < khi) asm volatile(\"s_waitcnt vmcnt(4)\\n\\ts_barrier\" ::: \"memory\");");
     k.line("else asm volatile(\"s_waitcnt vmcnt(0)\\n\\ts_barrier\" ::: \"memory\");");

@@ -62,7 +62,8 @@ def test_config_e_prefill_2048_then_32_greedy_steps(dev):
     print(f"config E: logits max rel err {worst:.3e} at the checked steps; "
           f"{ties} argmax ties (oracle gap within the tolerance), mismatches {mism}")
     assert not mism
-    assert ties <= (E.PROMPT + E.DECODE) // 100
+    # measured: 0 ties over the 2080 steps
+    assert ties <= 2
     # the cache rows at positions 0, 1024, 2047 and 2079 of every layer after the last step:
     # every element within one bf16 rounding step of the oracle's (2^-7 relative to the larger
     # of |e| and a quarter of the row's rms). Not bit-exact: the f32 path and the f64 oracle
@@ -73,7 +74,7 @@ def test_config_e_prefill_2048_then_32_greedy_steps(dev):
     # rows, none by more than one bf16 step of a typical element; the largest absolute
     # difference at a value near zero is 7.5e-4 at rms 0.9)
     total = off = 0
-    worst_rel = 0.0
+    worst_rel = worst_ref = 0.0
     for l in range(S.layers):
         kc = m.cache(l, "key")[:, f["cache_pos"], :].transpose(1, 0, 2)        # [4, kv, hd]
         vc = m.cache(l, "value")[:, :, f["cache_pos"]].transpose(2, 0, 1)      # [4, kv, hd]
@@ -83,9 +84,14 @@ def test_config_e_prefill_2048_then_32_greedy_steps(dev):
             rms = np.sqrt(np.mean(e ** 2, axis=-1, keepdims=True))
             rel = np.abs(g - e) / np.maximum(np.abs(e), 0.25 * rms)
             worst_rel = max(worst_rel, float(rel.max()))
+            # the reference's own metric (tests/metal.rs:99-105)
+            worst_ref = max(worst_ref, float(np.max(np.abs(g - e) / (1.0 + np.abs(e)))))
             total += got_bits.size
             off += int(np.count_nonzero(got_bits != want_bits))
     print(f"cache rows: {off} of {total} bf16 elements differ from the oracle's bits, "
-          f"max |g − e| / max(|e|, rms / 4) = {worst_rel:.3e}")
+          f"max |g − e| / max(|e|, rms / 4) = {worst_rel:.3e}, max |g − e| / (1 + |e|) = {worst_ref:.3e}")
+    # in the reference's metric: within 2e-3 (measured < 1e-3), a tenth of the bf16 bound
+    assert worst_ref <= 2e-3
     assert worst_rel <= 2.0 ** -7
-    assert off <= total * 15 // 100
+    # measured: 5114 of 65536 (7.8%) differ
+    assert off <= total * 10 // 100

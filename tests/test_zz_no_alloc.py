@@ -8,8 +8,8 @@ import pytest
 import oracle
 from sanic_amd import carrier as C
 from sanic_amd import configs, ir
-from sanic_amd.abi import SanicError
-from sanic_amd.program import OUTPUT, STREAM, Program, Sched
+from sanic_amd.abi import SanicError, lib
+from sanic_amd.program import OUTPUT, SCRATCH, STREAM, Program, Sched
 
 pytestmark = pytest.mark.gpu
 
@@ -22,8 +22,11 @@ def _both(dev, prog, vals):
     outs = {b.name: dev.alloc(b.nbytes) for b in prog.buffers if b.role == OUTPUT}
     for o in outs.values():
         o.upload(b"\xff" * o.nbytes)             # garbage the call must overwrite
+    before = lib().sanic_hip_device_allocations()
     exe.execute_static({**bufs, **outs})
+    allocated = lib().sanic_hip_device_allocations() - before
     got = {n: b.download() for n, b in outs.items()}
+    assert allocated == 0, f"execute_static made {allocated} device allocations"
     return want, got, exe
 
 
@@ -65,11 +68,9 @@ def test_execute_static_matches_execute_twice_second_smaller(dev, case):
 
 def test_execute_static_refuses_programs_beyond_its_scratch(dev):
     """Intermediates larger than the static scratch: a clear error, nothing launched."""
-    prog = configs.flash_prefill(32, 8, 4096)          # RoPE'd Q and K: 16 MiB + 4 MiB of intermediates
-    big = configs.flash_prefill(64, 16, 4096)          # twice that: beyond 32 MiB
+    big = configs.flash_prefill(64, 16, 4096)          # RoPE'd Q and K: 32 MiB + 8 MiB of intermediates
     exe = dev.prepare(big)
-    bufs = {b.name: dev.alloc(b.nbytes) for b in big.buffers if b.role != 3}
+    bufs = {b.name: dev.alloc(b.nbytes) for b in big.buffers if b.role != SCRATCH}
     with pytest.raises(SanicError) as e:
         exe.execute_static(bufs)
     assert "static scratch holds" in str(e.value)
-    del prog
