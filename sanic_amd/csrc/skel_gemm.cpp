@@ -161,6 +161,12 @@ std::vector<std::string> render_weight_run(const sanic_program_desc* d, int node
                                            std::vector<int>& dtypes, bool& ok, bool& contiguous, std::string& raw_bf16,
                                            bool stream);
 
+bool render_weight_affine(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
+                          const std::vector<int64_t>& ext, Code& lc, Code& dc, const std::string& nn,
+                          const std::string& k0, const std::string& sfx, std::vector<int>& bufs,
+                          std::vector<int>& dtypes, std::vector<std::string>& q, std::string& A, std::string& B,
+                          bool& negB, int64_t& uniform_div, bool stream);
+
 bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
     GemmPlan P;
     if (!gemm_plan(d, si, P)) return false;
@@ -173,10 +179,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     if (N % BN) return false;
     // 8 waves (4 × 2, two per SIMD) when the tile is 128 rows and at least 64 columns, so one
     // wave's LDS operand reads and global loads proceed under the other's MFMAs; else 4 (2 × 2)
-    const int NTH = (BM == 128 && BN >= 64) ? 512 : 256;
-    const int WGM = NTH / 128;                // waves along m (2 along n)
-    const int WM = BM / WGM, WN = BN / 2;     // per-wave tile
-    const int MT = WM / 16, NT = WN / 16;
+    int NTH = (BM == 128 && BN >= 64) ? 512 : 256;
     const int SR = (int)P.rslots.size();
     // k-contiguous tiles: unpadded 128-byte rows (64 bf16) with the 16-byte chunk index XORed
     // by (row mod 8) — a 72-element padded stride 2-way bank-conflicts the 16-row operand reads
@@ -193,7 +196,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         const sanic_node& n = d->nodes[st.leaf[leaf]];
         return n.kind == SANIC_NODE_INPUT && n.dtype == SANIC_BF16;
     };
-    const bool splitB = !raw_bf16_input(P.w);
+    bool splitB = !raw_bf16_input(P.w);
     bool splitA = true;
     {
         const sanic_expr& e = d->exprs[c.into[P.cslots[0]]];
@@ -242,6 +245,26 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         render_weight_run(d, st.leaf[P.w], cwt, {K, N}, l1, d1, "kk", "n0", "_p", tb, td, tok, tc, tr, false);
         bkn = tok && tc;
     }
+    // Grouped dequantization (packed 4-bit weights): the weight leaf is q·s ± z with q a packed
+    // 4-bit run and s, z constant over every 64-wide K tile (a quantization group of 64 or a
+    // multiple of it). Per tile, Σ_k x·w = s·Σ_k x·q ± z·Σ_k x, so the MFMA's B operand is q
+    // itself — small integers, exact in bf16: one MFMA per fragment instead of a hi + lo pair,
+    // and no dequantizing arithmetic ahead of the MFMAs — into a per-tile accumulator that the
+    // lanes fold into the output with their column's s and z and the rows' Σ x (the int4
+    // GEMV's per-run fold at tile granularity); Σ x comes from the matrix cores as well (the A
+    // fragment times a fragment of ones), not from VALU adds. Oracle: the same sum over
+    // w = q·s ± z in f64.
+    bool grouped = false;
+    bool gneg = false;
+    if (splitB && !bkn && contig && K % 64 == 0 && P.rslots.empty() && P.rows.size() == 1) {
+        std::vector<int> gb, gd;
+        std::vector<std::string> qv;
+        std::string A_, B_;
+        int64_t ud = 0;
+        Code l1, d1;
+        grouped = render_weight_affine(d, st.leaf[P.w], cw, {N, K}, l1, d1, "nn", "k0", "_g", gb, gd, qv, A_, B_, gneg, ud, false) &&
+                  ud % 64 == 0 && qv.size() == 8;
+    }
     const int BNS = BN + 8;                   // [k][n] B tile row stride (bf16)
     // row leaves vector forms over vars {0: m, 1: k}
     std::vector<std::vector<Sym>> crow;
@@ -261,6 +284,17 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         if (rr.empty()) rawA = false;
         crow.push_back(cr);
     }
+    if (!rawA) grouped = false;
+    if (grouped) splitB = false;
+    // grouped tiles: tiling variants {8 waves, load depth 4; 4 waves, depth 4; 8 waves, depth 2}
+    const int gvar = grouped && st.sched.variant > 0 && st.sched.variant < 3 ? st.sched.variant : 0;
+    if (grouped && BM == 128 && BN == 32 && gvar != 1) NTH = 512;
+    const int WGM = NTH / 128;                // waves along m (2 along n)
+    const int WM = BM / WGM, WN = BN / 2;     // per-wave tile
+    const int MT = WM / 16, NT = WN / 16;
+    // threads that load the B tile (all of them unless the tile has fewer runs of 8)
+    const int BTH = std::min(NTH, BN * 8);
+    const std::string btid = BTH < NTH ? "(tid % " + std::to_string(BTH) + ")" : std::string("tid");
 
     // A operands that need arithmetic (x·g of the fused RMSNorm) are built once by a first
     // launch into bf16 hi/lo planes [M][K] (plus the row slots), instead of by every one of the
@@ -334,6 +368,11 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     if (splitA) k.line("__shared__ unsigned short a_lo[2][" + std::to_string(BM * AS) + "];");
     if (splitB) k.line("__shared__ unsigned short b_lo[2][" + std::to_string(BTILE) + "];");
     if (SR) k.line("__shared__ float rs_lds[" + std::to_string(BM * SR) + "];");
+    if (grouped) {
+        k.line("__shared__ __attribute__((aligned(8))) float sz_lds[2][" + std::to_string(BN * 2) + "];");
+        // a B fragment of ones: the matrix cores also give each row's Σ x over the tile
+        k.line("const bf16x8 ones8 = __builtin_bit_cast(bf16x8, (sanic_u32x4){0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});");
+    }
     k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
     k.line("const int l16 = lane & 15, lq = lane >> 4;");
     k.line("const idx_t nb = blockIdx.x % " + std::to_string(N / BN) + ", mb = blockIdx.x / " + std::to_string(N / BN) + ";");
@@ -352,7 +391,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     const int RUNS_A = 64 / TPR / 8;       // runs of 8 per thread per tile
     // B tile: BN n × 64 k = BN·8 runs; k-contiguous weights: 8 lanes per row (coalesced rows),
     // else adjacent lanes take adjacent n
-    const int RUNS_B = BN * 8 / NTH;
+    const int RUNS_B = BN * 8 / BTH;
     auto emit_loads = [&](Code& c2, const std::string& kt0, const std::string& sfx) {
         // A runs
         c2.line("const idx_t mm" + sfx + " = m0 + tid / " + std::to_string(TPR) + ";");
@@ -392,21 +431,37 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             std::string nn, kk;
             if (bkn) {
                 // chunk c = tid + 256·r: k row c / (BN/8), 8 columns from (c % (BN/8))·8
-                const std::string cc = "(tid + " + std::to_string(r * NTH) + ")";
+                const std::string cc = "(" + btid + " + " + std::to_string(r * BTH) + ")";
                 kk = "(" + kt0 + " + " + cc + " / " + std::to_string(BN / 8) + ")";
                 nn = "(n0 + (" + cc + " % " + std::to_string(BN / 8) + ") * 8)";
             } else if (contig) {
-                nn = "(n0 + (tid / 8) + " + std::to_string(r * (NTH / 8)) + ")";
-                kk = "(" + kt0 + " + (tid % 8) * 8)";
+                nn = "(n0 + (" + btid + " / 8) + " + std::to_string(r * (BTH / 8)) + ")";
+                kk = "(" + kt0 + " + (" + btid + " % 8) * 8)";
             } else {
-                nn = "(n0 + (tid % " + std::to_string(BN) + "))";
-                kk = "(" + kt0 + " + ((tid / " + std::to_string(BN) + ") + " + std::to_string(r * (NTH / BN)) + ") * 8)";
+                nn = "(n0 + (" + btid + " % " + std::to_string(BN) + "))";
+                kk = "(" + kt0 + " + ((" + btid + " / " + std::to_string(BN) + ") + " + std::to_string(r * (BTH / BN)) + ") * 8)";
             }
             std::vector<int> rb, rd;
             bool rok = true, rc = true;
             std::string rr;
             Code l1, d1;
             l1.indent = d1.indent = c2.indent;
+            if (grouped) {
+                // q as exact bf16 integers; this row's group s and z for the lanes' fold
+                std::vector<std::string> qv;
+                std::string A_, B_;
+                bool nb = false;
+                int64_t ud = 0;
+                render_weight_affine(d, st.leaf[P.w], cw, {N, K}, l1, d1, nn, kk, "_b" + rs + sfx, rb, rd, qv, A_, B_, nb, ud, false);
+                for (size_t b = 0; b < rb.size(); b++)
+                    c2.line("const " + std::string(ctype_of(rd[b])) + "* __restrict__ wb" + std::to_string(b) + "_b" + rs + sfx + " = " + R.param(rb[b]) + ";");
+                c2.s << l1.str() << d1.str();
+                c2.line("const sanic_u32x4 rb" + rs + sfx + " = (sanic_u32x4){pk_bf16(" + qv[0] + ", " + qv[1] + "), pk_bf16(" + qv[2] + ", " +
+                        qv[3] + "), pk_bf16(" + qv[4] + ", " + qv[5] + "), pk_bf16(" + qv[6] + ", " + qv[7] + ")};");
+                c2.line("const float gs" + rs + sfx + " = " + A_ + ";");
+                c2.line("const float gz" + rs + sfx + " = " + (B_.empty() ? std::string("0.0f") : (nb ? "-" : "") + B_) + ";");
+                continue;
+            }
             auto vals = bkn ? render_weight_run(d, st.leaf[P.w], cwt, {K, N}, l1, d1, kk, nn, "_b" + rs + sfx, rb, rd, rok, rc, rr, false)
                             : render_weight_run(d, st.leaf[P.w], cw, {N, K}, l1, d1, nn, kk, "_b" + rs + sfx, rb, rd, rok, rc, rr, false);
             for (size_t b = 0; b < rb.size(); b++)
@@ -443,6 +498,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             const std::string aoff = koff("ar", "(tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8), AS);
             c2.line("*(sanic_u32x4*)(&a_lds[" + buf + "][" + aoff + "]) = rawa" + std::to_string(r) + sfx + ";");
         }
+
         for (int r = 0; r < RUNS_A && !pre && !rawA; r++) {
             std::string rs = std::to_string(r);
             // rest of the contraction slot (A) and the row slots, per element
@@ -474,26 +530,30 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
                         "), pk_bf16(" + av[4] + ", " + av[5] + "), pk_bf16(" + av[6] + ", " + av[7] + ")};");
             }
         }
+        if (BTH < NTH) c2.line("if (tid < " + std::to_string(BTH) + ") {");
         for (int r = 0; r < RUNS_B; r++) {
             std::string rs = std::to_string(r);
             std::string row, col;
             int stride = BS;
             if (bkn) {
-                const std::string cc = "(tid + " + std::to_string(r * NTH) + ")";
+                const std::string cc = "(" + btid + " + " + std::to_string(r * BTH) + ")";
                 row = "(" + cc + " / " + std::to_string(BN / 8) + ")";
                 col = "((" + cc + " % " + std::to_string(BN / 8) + ") * 8)";
                 stride = BNS;
             } else if (contig) {
-                row = "((tid / 8) + " + std::to_string(r * (NTH / 8)) + ")";
-                col = "((tid % 8) * 8)";
+                row = "((" + btid + " / 8) + " + std::to_string(r * (BTH / 8)) + ")";
+                col = "((" + btid + " % 8) * 8)";
             } else {
-                row = "(tid % " + std::to_string(BN) + ")";
-                col = "(((tid / " + std::to_string(BN) + ") + " + std::to_string(r * (NTH / BN)) + ") * 8)";
+                row = "(" + btid + " % " + std::to_string(BN) + ")";
+                col = "(((" + btid + " / " + std::to_string(BN) + ") + " + std::to_string(r * (BTH / BN)) + ") * 8)";
             }
             const std::string boff = bkn ? row + " * " + std::to_string(stride) + " + " + col : koff(row, col, stride);
             c2.line("*(sanic_u32x4*)(&b_lds[" + buf + "][" + boff + "]) = rb" + rs + sfx + ";");
             if (splitB) c2.line("*(sanic_u32x4*)(&b_lo[" + buf + "][" + boff + "]) = rl" + rs + sfx + ";");
+            if (grouped)
+                c2.line("if (tid % 8 == 0) *(sanic_f32x2*)(&sz_lds[" + buf + "][" + row + " * 2]) = (sanic_f32x2){gs" + rs + sfx + ", gz" + rs + sfx + "};");
         }
+        if (BTH < NTH) c2.line("}");
         c2.indent--;
         c2.line("}");
     };
@@ -540,20 +600,34 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             }
             c2.line("}");
         };
+        const std::string accv = grouped ? "tq" : "acc";
+        if (grouped) {
+            c2.line("f32x4 tq[" + MTs + "][" + NTs + "], xq[" + MTs + "];");
+            c2.line("#pragma unroll");
+            c2.line("for (int i = 0; i < " + MTs + "; ++i) {");
+            c2.line("  xq[i] = (f32x4){0, 0, 0, 0};");
+            c2.line("  #pragma unroll");
+            c2.line("  for (int j = 0; j < " + NTs + "; ++j) tq[i][j] = (f32x4){0, 0, 0, 0};");
+            c2.line("}");
+        }
         auto mfmas = [&](int ks) {
             const std::string kss = std::to_string(ks);
             c2.line("#pragma unroll");
             c2.line("for (int i = 0; i < " + MTs + "; ++i)");
             c2.line("  #pragma unroll");
             c2.line("  for (int j = 0; j < " + NTs + "; ++j) {");
-            c2.line("    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[" + kss + "][i], bf[" + kss + "][j], acc[i][j], 0, 0, 0);");
+            c2.line("    " + accv + "[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[" + kss + "][i], bf[" + kss + "][j], " + accv + "[i][j], 0, 0, 0);");
             if (splitA) c2.line("    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afl[" + kss + "][i], bf[" + kss + "][j], acc[i][j], 0, 0, 0);");
             if (splitB) c2.line("    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[" + kss + "][i], bfl[" + kss + "][j], acc[i][j], 0, 0, 0);");
             c2.line("  }");
+            if (grouped) {
+                c2.line("#pragma unroll");
+                c2.line("for (int i = 0; i < " + MTs + "; ++i) xq[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[" + kss + "][i], ones8, xq[i], 0, 0, 0);");
+            }
         };
         // instruction counts of one half: LDS reads and MFMAs
         const int nds = MT * (splitA ? 2 : 1) + NT * (bkn ? 2 : 1) * (splitB ? 2 : 1);
-        const int nmf = MT * NT * (1 + (splitA ? 1 : 0) + (splitB ? 1 : 0));
+        const int nmf = MT * NT * (1 + (splitA ? 1 : 0) + (splitB ? 1 : 0)) + (grouped ? MT : 0);
         reads(0);
         c2.line("__builtin_amdgcn_sched_barrier(0);");
         reads(1);
@@ -567,6 +641,19 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         if (nds > pairs) c2.line("__builtin_amdgcn_sched_group_barrier(0x100, " + std::to_string(nds - pairs) + ", 0);");
         c2.line("__builtin_amdgcn_sched_barrier(0);");
         mfmas(1);
+        if (grouped) {
+            // fold the tile: acc += s·Σ x·q ± z·Σ x (the sign rides z), per output element
+            c2.line("#pragma unroll");
+            c2.line("for (int i = 0; i < " + MTs + "; ++i) {");
+            c2.line("  const f32x4 xr = xq[i];");
+            c2.line("  #pragma unroll");
+            c2.line("  for (int j = 0; j < " + NTs + "; ++j) {");
+            c2.line("    const sanic_f32x2 sz = *(const sanic_f32x2*)(&sz_lds[" + buf + "][(wn + j * 16 + l16) * 2]);");
+            c2.line("    #pragma unroll");
+            c2.line("    for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(sz.y, xr[r], fmaf(sz.x, tq[i][j][r], acc[i][j][r]));");
+            c2.line("  }");
+            c2.line("}");
+        }
         c2.line("}");
     };
     const int64_t NKT = K / 64;
@@ -577,11 +664,18 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     k.indent--;
     k.line("}");
     k.line("__syncthreads();");
-    // Loads run two tiles ahead of the MFMAs: one workgroup per CU leaves a single wave per SIMD,
-    // so a tile's global loads (≈2 µs under load) must be in flight for two tiles' MFMAs, not
-    // one. Two register sets alternate in a loop unrolled by two; a set's loaded values are
-    // plain variables declared before the loop (the loads' address temporaries stay scoped).
-    const bool deep = NKT % 2 == 0 && NKT >= 4;
+    // Loads run DEPTH tiles ahead of the MFMAs: one workgroup per CU leaves a single wave per
+    // SIMD, so a tile's global loads (≈1–2 µs under load) must be in flight for several tiles'
+    // MFMAs, not one. DEPTH register sets rotate in a loop unrolled by DEPTH; a set's loaded
+    // values are plain variables declared before the loop (the loads' address temporaries stay
+    // scoped). Set u holds the tiles ≡ u (mod DEPTH): at step t the set of tile t (already in
+    // LDS) takes tile t + DEPTH, and the set of tile t + 1 goes to LDS behind the MFMAs.
+    // Depth 2 for bf16 tiles; 4 for grouped 4-bit tiles, whose per-tile MFMA work is small
+    // against the load latency. Variant 1 takes the other depth.
+    int DEPTH = grouped ? (gvar == 2 ? 2 : 4) : 2;
+    if (!grouped && st.sched.variant == 1) DEPTH = 4;
+    if (NKT % DEPTH || NKT < 2 * DEPTH) DEPTH = 2;
+    const bool deep = NKT % DEPTH == 0 && NKT >= 2 * DEPTH;
     if (deep) {
         auto persistent = [&](const std::string& sfx, Code& decl) {
             Code tmp;
@@ -594,7 +688,8 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
                 const std::string name = (*it)[2];
                 if (name.size() > sfx.size() && name.compare(name.size() - sfx.size(), sfx.size(), sfx) == 0 &&
                     (name.rfind("pah", 0) == 0 || name.rfind("pal", 0) == 0 || name.rfind("rb", 0) == 0 ||
-                     name.rfind("rl", 0) == 0 || name.rfind("ra", 0) == 0) && name.rfind("rbh", 0) != 0 &&
+                     name.rfind("rl", 0) == 0 || name.rfind("ra", 0) == 0 || name.rfind("gs", 0) == 0 ||
+                     name.rfind("gz", 0) == 0) && name.rfind("rbh", 0) != 0 &&
                     name.rfind("rbl", 0) != 0 && !seen.count(name)) {
                     seen.insert(name);
                     decl.line(std::string((*it)[1]) + " " + name + ";");
@@ -623,27 +718,30 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         };
         Code decl;
         decl.indent = k.indent;
-        auto names_p = persistent("_p", decl);
-        auto names_q = persistent("_q", decl);
+        std::vector<std::set<std::string>> names(DEPTH);
+        auto set_sfx = [](int u) { return "_s" + std::to_string(u); };
+        for (int u = 0; u < DEPTH; u++) names[u] = persistent(set_sfx(u), decl);
         k.s << decl.str();
-        load_into("(idx_t)64", "_p", names_p);                      // tile 1
-        const std::string N2 = std::to_string(NKT);
-        k.line("for (idx_t kt = 0; kt < " + N2 + "; kt += 2) {");
+        for (int u = 1; u < DEPTH; u++) load_into("(idx_t)" + std::to_string(64 * u), set_sfx(u), names[u]);   // tiles 1..DEPTH-1
+        const std::string N2 = std::to_string(NKT), DS = std::to_string(DEPTH);
+        k.line("for (idx_t kt = 0; kt < " + N2 + "; kt += " + DS + ") {");
         k.indent++;
-        // even step: set p holds tile kt+1; tile kt+2 → set q
-        load_into("(((kt + 2) % " + N2 + ") * 64)", "_q", names_q);
-        emit_mfma(k, "0");
-        emit_stores(k, "1", "_p");
-        k.line("__syncthreads();");
-        // odd step: set q holds tile kt+2; tile kt+3 → set p
-        load_into("(((kt + 3) % " + N2 + ") * 64)", "_p", names_p);
-        emit_mfma(k, "1");
-        k.line("if (kt + 2 < " + N2 + ") {");
-        k.indent++;
-        emit_stores(k, "0", "_q");
-        k.indent--;
-        k.line("}");
-        k.line("__syncthreads();");
+        for (int u = 0; u < DEPTH; u++) {
+            // step kt+u: tile kt+u is in LDS buffer u % 2; its set takes tile kt+u+DEPTH
+            load_into("(((kt + " + std::to_string(u + DEPTH) + ") % " + N2 + ") * 64)", set_sfx(u), names[u]);
+            emit_mfma(k, std::to_string(u % 2));
+            const int nx = (u + 1) % DEPTH;
+            if (u == DEPTH - 1) {
+                k.line("if (kt + " + DS + " < " + N2 + ") {");
+                k.indent++;
+            }
+            emit_stores(k, std::to_string((u + 1) % 2), set_sfx(nx));
+            if (u == DEPTH - 1) {
+                k.indent--;
+                k.line("}");
+            }
+            k.line("__syncthreads();");
+        }
         k.indent--;
         k.line("}");
     } else {
@@ -729,10 +827,12 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     src << R.args_struct(pre ? std::vector<std::string>{"float* __restrict__ scratch"} : std::vector<std::string>{});
     if (pre) src << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "_pre(Args a) {\n" << R.entry() << kp.str() << "}\n";
     src << "extern \"C\" __global__ void __launch_bounds__(" << NTH << ") " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
-    out.kernel_kind = "skeleton:gemm[" + std::to_string(BM) + "x" + std::to_string(BN) + (splitA ? ",a2" : "") + (splitB ? ",b2" : "") + (bkn ? ",kn" : "") + (pre ? ",pre" : "") + "]";
+    out.kernel_kind = "skeleton:gemm[" + std::to_string(BM) + "x" + std::to_string(BN) + (splitA ? ",a2" : "") + (splitB ? ",b2" : "") +
+                      (grouped ? ",grp" : "") + (bkn ? ",kn" : "") + (pre ? ",pre" : "") + (deep ? ",d" + std::to_string(DEPTH) : "") + ",w" + std::to_string(NTH / 64) + "]";
+    out.variants = grouped ? 3 : 2;
     // dequantized-weight tiles (int4): the ILP-maximising machine scheduler, D2 25.1 → 22.9 µs;
     // bf16 tiles keep the default strategy (no measurable difference)
-    out.source = (splitB ? std::string("// sched-strategy: iterative-ilp\n") : std::string()) + src.str();
+    out.source = (splitB || grouped ? std::string("// sched-strategy: iterative-ilp\n") : std::string()) + src.str();
     std::vector<Arg> args = R.arg_list();
     if (pre) {
         args.push_back({Arg::SCRATCH, 0});

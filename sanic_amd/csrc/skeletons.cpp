@@ -10,6 +10,7 @@
 //             per workgroup, per-row partials merge across the wave by shuffles. Consecutive
 //             stages with the same row leaves are batched into one launch (q/k/v, gate/up).
 //   rowwrite  the in-place `where(at_pos, new, cache)` stage: launched over the cache row only.
+#include <numeric>
 #include <algorithm>
 #include <cmath>
 #include <set>
@@ -218,6 +219,9 @@ struct VecW {
     std::string last_raw;     // the 128-bit bf16 register of the last contiguous access
     bool stream = true;           // weights are read once: non-temporal loads
     bool byte_split = false;      // packed 4-bit runs through byte-to-float converts
+    // gcd of the k divisors of every access that does not move within a run (0: none moves
+    // with k at all): such an access is constant over every aligned block of that many k
+    int64_t uniform_div = 0;
     std::string ld(const std::string& ty, const std::string& ptr) const {
         return stream ? "__builtin_nontemporal_load((const " + ty + "*)(" + ptr + "))" : "*(const " + ty + "*)(" + ptr + ")";
     }
@@ -279,6 +283,8 @@ struct VecW {
         lc.line("const idx_t " + base + " = " + addr + ";");
         const char* comp[4] = {"x", "y", "z", "w"};
         if (jstride == 0) {
+            for (auto& t : acc.addr.terms)
+                if (t.var == 1) uniform_div = std::gcd(uniform_div, t.div);
             std::string v = fresh("w");
             lc.line("const float " + v + " = " + one(base) + ";");
             return std::vector<std::string>(8, v);
@@ -411,6 +417,29 @@ std::vector<std::string> render_weight_run(const sanic_program_desc* d, int node
     int kind = d->nodes[node].kind;
     raw_bf16 = (bufs.size() == 1 && dtypes[0] == SANIC_BF16 && kind != SANIC_NODE_MAP && kind != SANIC_NODE_CONST) ? vw.last_raw : "";
     return vals;
+}
+
+// One run of 8 of a weight leaf of the form q·A ± B (q a packed 4-bit run, A and B constant
+// over the run) at (nn, k0): q's 8 values, A and B (B empty when absent; negB for q·A − B).
+// `uniform_div`: A and B are constant over every aligned block of that many k (0: over all k).
+bool render_weight_affine(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
+                          const std::vector<int64_t>& ext, Code& lc, Code& dc, const std::string& nn,
+                          const std::string& k0, const std::string& sfx, std::vector<int>& bufs,
+                          std::vector<int>& dtypes, std::vector<std::string>& q, std::string& A, std::string& B,
+                          bool& negB, int64_t& uniform_div, bool stream) {
+    VecW vw{d};
+    vw.stream = stream;
+    vw.nn = nn;
+    vw.k0 = k0;
+    vw.ptr = "wb";
+    vw.psfx = sfx;
+    vw.sfx = sfx;
+    negB = false;
+    const bool ok = vw.render_affine(lc, dc, node, c, ext, q, A, B, negB) && vw.ok;
+    bufs = vw.bufs;
+    dtypes = vw.dtypes;
+    uniform_div = vw.uniform_div;
+    return ok;
 }
 
 // ───────────────────────── gemv ───────────────────────────────────────────────────────────

@@ -18,6 +18,7 @@ def _report(exe, got, want):
     print(exe.stage_kernel(0), float(rel.max()), "bad", len(bad), bad[:8].tolist(), flush=True)
 
 
+@pytest.mark.parametrize("variant", [0, 1])
 @pytest.mark.parametrize("M,K,N,kmajor", [
     (512, 2048, 8192, True),      # config B2, W [K, N]
     (512, 2048, 8192, False),     # same with the reference's [out, in] layout
@@ -28,8 +29,8 @@ def _report(exe, got, want):
     (256, 384, 8192, False),      # 8-wave tiles, [out, in] weights, in-kernel row slots
     (128, 1536, 2048, True),      # operand-building launch with 3 k chunks over 4 waves
 ])
-def test_rmsnorm_gemm(dev, M, K, N, kmajor):
-    prog = configs.rmsnorm_projection(M=M, K=K, N=N, kmajor=kmajor)
+def test_rmsnorm_gemm(dev, M, K, N, kmajor, variant):
+    prog = configs.rmsnorm_projection(M=M, K=K, N=N, kmajor=kmajor).with_variants({0: variant})
     x = _bf16_vals(301, M * K).reshape(M, K)
     g = _bf16_vals(302, K, 1.0, 0.02)
     wbits = oracle.synth_bf16(303, N * K, "normal", 0.0, 0.02)
@@ -43,14 +44,25 @@ def test_rmsnorm_gemm(dev, M, K, N, kmajor):
     assert err < 2e-2
 
 
-@pytest.mark.parametrize("M,K,N,G", [(128, 2048, 8192, 64), (64, 512, 256, 32), (256, 512, 8192, 64)])
-def test_int4_gemm(dev, M, K, N, G):
+@pytest.mark.parametrize("M,K,N,G,zk,variant", [
+    (128, 2048, 8192, 64, "8s", 0),      # config D2: grouped tiles (q on the MFMA, s/z folded per tile)
+    (128, 2048, 8192, 64, "8s", 1),      # the other load depth
+    (64, 512, 256, 32, "8s", 0),         # groups narrower than a K tile: hi + lo dequantized B
+    (256, 512, 8192, 64, "8s", 0),
+    (128, 1024, 512, 128, "any", 0),     # groups of two K tiles, zero points unrelated to s
+    (64, 512, 256, 64, "any", 1),
+    (128, 2048, 8192, 64, "any", 2),
+])
+def test_int4_gemm(dev, M, K, N, G, zk, variant):
     """Config D2: packed uint4 [N, K], per-group scale and zero point, w = u·s − z."""
-    prog = configs.int4_matmul(M=M, K=K, N=N, G=G)
+    prog = configs.int4_matmul(M=M, K=K, N=N, G=G).with_variants({0: variant})
     rng = np.random.default_rng(11)
     u = rng.integers(0, 16, size=(N, K))
     s = _bf16_vals(401, N * K // G, 0.001, 0.02, kind="uniform").reshape(N, K // G)
-    z = np.array([oracle.round_bf16(8.0 * v) for v in s.reshape(-1)]).reshape(s.shape)
+    if zk == "8s":
+        z = np.array([oracle.round_bf16(8.0 * v) for v in s.reshape(-1)]).reshape(s.shape)
+    else:
+        z = _bf16_vals(403, N * K // G, -0.1, 0.1, kind="uniform").reshape(s.shape)
     x = _bf16_vals(402, M * K).reshape(M, K)
     got, exe = run_on_gpu(dev, prog, {"x": x, "Wq": u.reshape(N, K // G, G), "S": s, "Z": z})
     packed = (u[:, 0::2] | (u[:, 1::2] << 4)).astype(np.uint8)
@@ -58,4 +70,5 @@ def test_int4_gemm(dev, M, K, N, G):
     err = bf16_rel(got["y"], want)
     _report(exe, got["y"], want)
     assert exe.stage_kernel(0).startswith("skeleton:gemm")
+    assert ("grp" in exe.stage_kernel(0)) == (G % 64 == 0)
     assert err < 2e-2
