@@ -55,8 +55,8 @@ def test_lowering_chooses_the_expected_kernel(name):
         "B1_rows": (configs.rmsnorm_projection(kmajor=False), 0, "skeleton:gemv"),
         "D1": (configs.int4_matmul(), 0, "skeleton:gemv"),
         "C3": (configs.decode_attention(), 0, "skeleton:attn_decode"),
-        "B2": (configs.rmsnorm_projection(M=512), 0, "skeleton:gemm[128x128,a2,kn,pre]"),
-        "D2": (configs.int4_matmul(M=128), 0, "skeleton:gemm"),
+        "B2": (configs.rmsnorm_projection(M=512), 0, "skeleton:gemm[128x128,a2,kn,pre,"),
+        "D2": (configs.int4_matmul(M=128), 0, "skeleton:gemm[128x32,grp,"),
         "C1": (configs.flash_prefill(), 2, "skeleton:flash_prefill"),
         # q/k/v batched into one launch; this step's K/V cache writes done by the attention kernel
         "E_qkv": (configs.llama_decode(), 1, "skeleton:gemv[batched 3]"),
