@@ -37,16 +37,22 @@ def flash_prefill(NH: int = 32, NKV: int = 8, S: int = 4096, HD: int = 64, theta
     sliding-window mask (key visible iff q − window + 1 ≤ k ≤ q). The RoPE'd Q and K are
     materialised by two pointwise stages (bf16), then one FlashAttention carrier fold.
     `v_transposed` stores V as [NKV, HD, S] (keys contiguous, the decode cache's layout) and
-    reads it through a transposed view."""
+    reads it through a transposed view.
+
+    With RoPE the rotation of each (row, frequency) is materialised once (`rope_table`, f32
+    [S, 2, HD/2]) for every head; K is rotated by a pointwise stage (bf16: every query block
+    reads each key row, so it is rotated once, not per reader), and Q's rotation stays inside
+    the fold's score leaf (the reference's in-body leaf, nn.rs:176-194), where each query row is
+    read once."""
     p = Program()
     q = p.input("Q", (NH, S, HD), ir.BF16)
     k = p.input("K", (NKV, S, HD), ir.BF16)
     v = ir.transpose(p.input("V", (NKV, HD, S), ir.BF16), 1, 2) if v_transposed else p.input("V", (NKV, S, HD), ir.BF16)
     if rope_stages:
         invf = ir.rope_inv_freq(theta, HD // 2)
-        rows = ir.iota(S)
-        q = p.pointwise("Qr", ir.rope(q, rows, invf), ir.BF16, role=3)
-        k = p.pointwise("Kr", ir.rope(k, rows, invf), ir.BF16, role=3)
+        table = p.pointwise("rope.table", ir.rope_table(ir.iota(S), invf), ir.F32, role=3)
+        q = ir.rope_tabled(q, table)
+        k = p.pointwise("Kr", ir.rope_tabled(k, table), ir.BF16, role=3)
     rep = NH // NKV
     scores = ir.reduce(ir.map_(ir.MUL, ir.unsqueeze(q, 2), ir.unsqueeze(ir.expand_heads(k, 0, rep), 1)), 3, ir.M_ADD)
     scores = ir.map_(ir.MUL, scores, ir.const(1.0 / math.sqrt(HD)))            # [NH, S, S]

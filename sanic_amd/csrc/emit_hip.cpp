@@ -1301,9 +1301,67 @@ LoweredStage lower_generic_fold(const sanic_program_desc* d, int si, int64_t& sc
     return L;
 }
 
+static bool stage_touches_q8(const sanic_program_desc* d, int s);
+
+// Elementwise stage as runs of 8 along its innermost dim: each thread renders 8 consecutive
+// outputs with wide loads (render_run) and stores them with one 16-byte (bf16) or two (f32)
+// stores. For stages without a `where`, bf16/f32 outputs and an innermost extent that is a
+// multiple of 8; the values are the scalar renderer's, element for element.
+static bool lower_pointwise_runs(const sanic_program_desc* d, int si, LoweredStage& L) {
+    const sanic_stage& st = d->stages[si];
+    if (st.where >= 0 || st.rank < 1 || st.grid[st.rank - 1] % 8) return false;
+    const int odt = st.out_dtype;
+    if ((odt != SANIC_BF16 && odt != SANIC_F32) || d->buffers[st.out_buffer].dtype != odt) return false;
+    const sanic_node& vn = d->nodes[st.value];
+    std::vector<Sym> c(vn.rank);
+    const int lead = st.rank - vn.rank;
+    for (int j = 0; j < vn.rank; j++) c[j] = vn.shape[j] == 1 ? Sym() : Sym::var(lead + j);
+    std::vector<std::string> vars;
+    std::vector<int64_t> ext;
+    for (int j = 0; j < st.rank; j++) {
+        vars.push_back("g" + std::to_string(j));
+        ext.push_back(st.grid[j]);
+    }
+    Code lc, dc;
+    lc.indent = dc.indent = 1;
+    std::vector<int> bufs, dts;
+    bool ok = true;
+    auto vals = render_run(d, st.value, c, ext, vars, st.rank - 1, lc, dc, "_r", bufs, dts, ok);
+    if (!ok || vals.size() != 8) return false;
+    Renderer R(d);
+    Code body;
+    body.indent = 1;
+    const int64_t gvol = vol(st.grid, st.rank), runs = gvol / 8;
+    body.line("const idx_t gr = (idx_t)blockIdx.x * 256 + threadIdx.x;");
+    body.line("if (gr >= " + std::to_string(runs) + ") return;");
+    body.line("const idx_t gid = gr * 8;");
+    decode_grid(body, st, "gid");
+    for (size_t b = 0; b < bufs.size(); b++)
+        body.line("const " + std::string(ctype_of(dts[b])) + "* __restrict__ rb" + std::to_string(b) + "_r = " + R.param(bufs[b]) + ";");
+    body.s << lc.str() << dc.str();
+    const std::string out = R.param(st.out_buffer);
+    if (odt == SANIC_BF16) {
+        std::string w = "(sanic_u32x4){";
+        for (int q = 0; q < 4; q++)
+            w += std::string(q ? ", " : "") + "(unsigned)sanic_to_bf16(" + vals[2 * q] + ") | ((unsigned)sanic_to_bf16(" + vals[2 * q + 1] + ") << 16)";
+        body.line("*(sanic_u32x4*)(" + out + " + gid) = " + w + "};");
+    } else {
+        body.line("*(sanic_f32x4*)(" + out + " + gid) = (sanic_f32x4){" + vals[0] + ", " + vals[1] + ", " + vals[2] + ", " + vals[3] + "};");
+        body.line("*(sanic_f32x4*)(" + out + " + gid + 4) = (sanic_f32x4){" + vals[4] + ", " + vals[5] + ", " + vals[6] + ", " + vals[7] + "};");
+    }
+    std::ostringstream src;
+    src << kPrelude << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(256) sanic_pointwise_x8(Args a) {\n"
+        << R.entry() << body.str() << "}\n";
+    L.kernel_kind = "pointwise:runs8";
+    L.source = src.str();
+    L.launches.push_back({"sanic_pointwise_x8", "", dim3((unsigned)((runs + 255) / 256)), dim3(256), 0, R.arg_list()});
+    return true;
+}
+
 LoweredStage lower_pointwise(const sanic_program_desc* d, int si) {
     const sanic_stage& st = d->stages[si];
     LoweredStage L;
+    if (!getenv("SANIC_HIP_GENERIC") && !stage_touches_q8(d, si) && lower_pointwise_runs(d, si, L)) return L;
     L.kernel_kind = st.where >= 0 ? "pointwise:in-place-where" : "pointwise";
     Renderer R(d);
     Code body;

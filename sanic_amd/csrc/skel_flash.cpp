@@ -43,7 +43,24 @@ struct FlashPlan {
     int rep = 1;
     int dot_reduce = -1;
     Access qacc, kacc, vacc;
+    // a query side that is an elementwise expression (RoPE'd Q, say) rather than one affine
+    // view: rendered per element once per workgroup, at coordinates qcoords over the vars
+    // {0: head, 1: key, 2: d, 3: query row}
+    bool qexpr = false;
+    int qnode = -1;
+    std::vector<Sym> qcoords;
 };
+
+bool has_reduce_below(const sanic_program_desc* d, int node) {
+    std::vector<int> st{node};
+    while (!st.empty()) {
+        int i = st.back();
+        st.pop_back();
+        if (d->nodes[i].kind == SANIC_NODE_REDUCE || d->nodes[i].kind == SANIC_NODE_SCAN) return true;
+        for (int q = 0; q < d->nodes[i].n_in; q++) st.push_back(d->nodes[i].in[q]);
+    }
+    return false;
+}
 
 bool sym_is_var(const Sym& s, int& var) {
     if (s.c0 != 0 || s.terms.size() != 1) return false;
@@ -120,7 +137,12 @@ bool find_flash_dot(const sanic_program_desc* d, int node, const std::vector<Sym
     }
     if (kside < 0) return false;
     if (!sym_access(d, mp.in[kside], cc[kside], ext4, P.kacc)) return false;
-    if (!sym_access(d, mp.in[1 - kside], cc[1 - kside], ext4, P.qacc)) return false;
+    if (!sym_access(d, mp.in[1 - kside], cc[1 - kside], ext4, P.qacc)) {
+        if (has_reduce_below(d, mp.in[1 - kside])) return false;
+        P.qexpr = true;
+        P.qnode = mp.in[1 - kside];
+        P.qcoords = cc[1 - kside];
+    }
     P.dot_reduce = node;
     P.HD = mp.shape[n.dim];
     return true;
@@ -194,16 +216,16 @@ bool flash_plan(const sanic_program_desc* d, int si, FlashPlan& P) {
         vcs[j] = b == SANIC_BIND_STREAM ? Sym::var(1) : b == P.hdim ? Sym::var(0) : b == P.edim ? Sym::var(2) : Sym();
     }
     if (!sym_access(d, st.leaf[P.vleaf], vcs, {P.NH, P.T, P.E}, P.vacc)) return false;
-    if (P.qacc.dtype != SANIC_BF16 || P.kacc.dtype != SANIC_BF16 || P.vacc.dtype != SANIC_BF16) return false;
+    if ((!P.qexpr && P.qacc.dtype != SANIC_BF16) || P.kacc.dtype != SANIC_BF16 || P.vacc.dtype != SANIC_BF16) return false;
     if (P.HD != 64 || P.E != 64 || P.NQ % 128 != 0 || P.T % 64 != 0) return false;
     // Q: (h, d, i) with d contiguous; K: (⌊h/rep⌋, t, d) with d contiguous; V: (⌊h/rep⌋, t, e)
     std::vector<int64_t> qc, kc, vc;
     int qh, kh, vh;
     int64_t qhc, khc, vhc;
-    if (!split_addr(P.qacc.addr, 4, qc, qh, qhc) || qh != 0) return false;
+    if (!P.qexpr && (!split_addr(P.qacc.addr, 4, qc, qh, qhc) || qh != 0 || qc[2] != 1 || qc[1] != 0)) return false;
     if (!split_addr(P.kacc.addr, 4, kc, kh, khc)) return false;
     if (!split_addr(P.vacc.addr, 3, vc, vh, vhc)) return false;
-    if (qc[2] != 1 || qc[1] != 0 || kc[2] != 1 || kc[3] != 0 || (vc[2] != 1 && vc[1] != 1)) return false;
+    if (kc[2] != 1 || kc[3] != 0 || (vc[2] != 1 && vc[1] != 1)) return false;
     int repk = kh ? kh : (kc[0] ? 1 : (int)P.NH);
     int repv = vh ? vh : (vc[0] ? 1 : (int)P.NH);
     if (repk != repv) return false;
@@ -249,7 +271,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     std::vector<int64_t> qc, kc, vc;
     int qh, kh, vh;
     int64_t qhc, khc, vhc;
-    split_addr(P.qacc.addr, 4, qc, qh, qhc);
+    if (!P.qexpr) split_addr(P.qacc.addr, 4, qc, qh, qhc);
     split_addr(P.kacc.addr, 4, kc, kh, khc);
     split_addr(P.vacc.addr, 3, vc, vh, vhc);
     const bool v_rows = vc[2] == 1;                  // V[t, e] rows (else V^T with t contiguous)
@@ -325,7 +347,16 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         fo.line(store_stmt(Ro.param(st.out_buffer), lin, st.out_dtype, v, false, d->buffers[st.out_buffer].scale));
     }
     for (int b : Ro.bufs) R.param(b);
-    std::string qp = R.param(P.qacc.buffer), kp = R.param(P.kacc.buffer), vp = R.param(P.vacc.buffer);
+    if (P.qexpr) {
+        // register the expression's buffers before the argument struct is written
+        Code scratch_code;
+        R.memo.emplace_back();
+        std::vector<std::string> cs;
+        for (auto& sy : P.qcoords) cs.push_back(sy.render({"hh", "(idx_t)0", "dd", "qrow"}));
+        R.value(scratch_code, P.qnode, cs);
+        R.memo.pop_back();
+    }
+    std::string qp = P.qexpr ? std::string() : R.param(P.qacc.buffer), kp = R.param(P.kacc.buffer), vp = R.param(P.vacc.buffer);
 
     std::ostringstream src;
     src << kPrelude;
@@ -447,12 +478,77 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // Q^T as the B operand (lane = query column l16 (+16·qt), d-slots lq·8 + 0..7 (+32·ds)),
     // held in registers for the whole key loop, loaded once from global memory
     k.line("bf16x8 qf[2][2];");
-    k.line("#pragma unroll");
-    k.line("for (int qt = 0; qt < 2; ++qt)");
-    k.line("  #pragma unroll");
-    k.line("  for (int ds = 0; ds < 2; ++ds)");
-    k.line("    qf[qt][ds] = *(const bf16x8*)(" + qp + " + " + std::to_string(P.qacc.addr.c0) + " + " + hterm(qc, qh, qhc) +
-           " + (q0 + qt * 16 + l16) * " + std::to_string(qc[3]) + " + (ds * 4 + lq) * 8);");
+    if (!P.qexpr) {
+        k.line("#pragma unroll");
+        k.line("for (int qt = 0; qt < 2; ++qt)");
+        k.line("  #pragma unroll");
+        k.line("  for (int ds = 0; ds < 2; ++ds)");
+        k.line("    qf[qt][ds] = *(const bf16x8*)(" + qp + " + " + std::to_string(P.qacc.addr.c0) + " + " + hterm(qc, qh, qhc) +
+               " + (q0 + qt * 16 + l16) * " + std::to_string(qc[3]) + " + (ds * 4 + lq) * 8);");
+    }
+    // An expression query side is rendered element by element (the lane's 2 × 16 values), once
+    // per workgroup, after the first K/V transfers are requested so its loads and arithmetic
+    // overlap them; each value goes to the MFMA rounded to bf16 (RNE), the operand width.
+    // The vectorised form's loads go out first, where the plain Q load would (loads complete in
+    // issue order, so the rotation's operands are not queued behind the first K/V tiles), and
+    // its arithmetic after the transfers are requested; the per-element form runs after them.
+    Code q_lc, q_dc;
+    bool q_runs = false;
+    std::vector<std::string> q_vals[2][2];
+    if (P.qexpr) {
+        q_lc.indent = q_dc.indent = k.indent + 1;
+        bool ok = true;
+        for (int qt = 0; qt < 2 && ok; qt++)
+            for (int ds = 0; ds < 2 && ok; ds++) {
+                const std::string sfx = "_q" + std::to_string(qt) + std::to_string(ds);
+                const std::vector<std::string> vars = {"hh", "(idx_t)0", "((idx_t)lq * 8 + " + std::to_string(ds * 32) + ")",
+                                                       "(q0 + " + std::to_string(qt * 16) + " + l16)"};
+                std::vector<int> bufs, dts;
+                Code pl;
+                pl.indent = q_lc.indent;
+                q_vals[qt][ds] = render_run(d, P.qnode, P.qcoords, {NH, T, HD, NQ}, vars, 2, q_lc, q_dc, sfx, bufs, dts, ok);
+                for (size_t b = 0; b < bufs.size() && ok; b++)
+                    k.line("const " + std::string(ctype_of(dts[b])) + "* __restrict__ rb" + std::to_string(b) + sfx + " = " + R.param(bufs[b]) + ";");
+            }
+        q_runs = ok;
+        // the loads right away, as the plain Q load would be
+        if (q_runs) k.s << q_lc.str();
+    }
+    auto emit_qexpr = [&]() {
+        if (q_runs) {
+            k.s << q_dc.str();
+            for (int qt = 0; qt < 2; qt++)
+                for (int ds = 0; ds < 2; ds++) {
+                    const auto& v = q_vals[qt][ds];
+                    k.line("qf[" + std::to_string(qt) + "][" + std::to_string(ds) + "] = __builtin_bit_cast(bf16x8, (sanic_u32x4){pk_bf16(" + v[0] + ", " + v[1] +
+                           "), pk_bf16(" + v[2] + ", " + v[3] + "), pk_bf16(" + v[4] + ", " + v[5] + "), pk_bf16(" + v[6] + ", " + v[7] + ")});");
+                }
+            return;
+        }
+        for (int qt = 0; qt < 2; qt++) {
+            k.line("{");
+            k.indent++;
+            k.line("const idx_t qrow = q0 + " + std::to_string(qt * 16) + " + l16;");
+            R.memo.emplace_back();
+            std::string vals[2][8];
+            for (int ds = 0; ds < 2; ds++)
+                for (int j = 0; j < 8; j++) {
+                    const std::string dd = "((idx_t)lq * 8 + " + std::to_string(ds * 32 + j) + ")";
+                    std::vector<std::string> cs;
+                    for (auto& sy : P.qcoords) cs.push_back(sy.render({"hh", "(idx_t)0", dd, "qrow"}));
+                    vals[ds][j] = R.value(k, P.qnode, cs);
+                }
+            R.memo.pop_back();
+            for (int ds = 0; ds < 2; ds++) {
+                std::string pk = "(sanic_u32x4){";
+                for (int q = 0; q < 4; q++)
+                    pk += std::string(q ? ", " : "") + "pk_bf16(" + vals[ds][2 * q] + ", " + vals[ds][2 * q + 1] + ")";
+                k.line("qf[" + std::to_string(qt) + "][" + std::to_string(ds) + "] = __builtin_bit_cast(bf16x8, " + pk + "});");
+            }
+            k.indent--;
+            k.line("}");
+        }
+    };
     k.line("f32x4 o[4][2];");
     k.line("#pragma unroll");
     k.line("for (int dt = 0; dt < 4; ++dt) { o[dt][0] = (f32x4){0, 0, 0, 0}; o[dt][1] = (f32x4){0, 0, 0, 0}; }");
@@ -496,6 +592,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.indent++;
     k.line("fetch(klo, 0);");
     k.line("if (klo + 64 < khi) fetch(klo + 64, 1);");
+    if (P.qexpr) emit_qexpr();
     k.line("int buf = 0;");
     k.line("for (idx_t t0 = klo; t0 < khi; t0 += 64) {");
     k.indent++;

@@ -222,6 +222,11 @@ struct VecW {
     // gcd of the k divisors of every access that does not move within a run (0: none moves
     // with k at all): such an access is constant over every aligned block of that many k
     int64_t uniform_div = 0;
+    // general form: the coordinate variables' names and which of them the run of 8 moves
+    // along (default: {nn, k0}, runs along var 1)
+    std::vector<std::string> vars;
+    int kv = 1;
+    std::vector<std::string> names() const { return vars.empty() ? std::vector<std::string>{nn, k0} : vars; }
     std::string ld(const std::string& ty, const std::string& ptr) const {
         return stream ? "__builtin_nontemporal_load((const " + ty + "*)(" + ptr + "))" : "*(const " + ty + "*)(" + ptr + ")";
     }
@@ -230,6 +235,22 @@ struct VecW {
     std::vector<std::string> render(Code& lc, Code& dc, int node, const std::vector<Sym>& c, const std::vector<int64_t>& ext) {
         const sanic_node& n = d->nodes[node];
         if (n.kind == SANIC_NODE_CONST) return std::vector<std::string>(8, flit(n.value));
+        if (n.kind == SANIC_NODE_IOTA || n.kind == SANIC_NODE_COORDINATE) {
+            // the coordinate's own value: one value per run when it does not move within an
+            // aligned run of 8, else base + j·coef when it moves by a constant step
+            const Sym& cs = c[n.kind == SANIC_NODE_IOTA ? 0 : n.dim];
+            int64_t step = 0;
+            for (auto& t : cs.terms) {
+                if (t.var != kv) continue;
+                if (t.div == 1 && t.mod == 0) step += t.coef;
+                else if (t.div % 8 != 0 || (t.div == 1 && t.mod % 8 != 0)) { ok = false; return {}; }
+            }
+            std::string base = fresh("ci");
+            lc.line("const float " + base + " = (float)(" + cs.render(names()) + ");");
+            std::vector<std::string> out(8);
+            for (int j = 0; j < 8; j++) out[j] = step == 0 ? base : "(" + base + " + " + flit((double)(step * j)) + ")";
+            return out;
+        }
         if (n.kind == SANIC_NODE_MAP) {
             std::vector<std::string> a[3];
             for (int k = 0; k < n.n_in; k++) {
@@ -257,7 +278,7 @@ struct VecW {
         if (!sym_access(d, node, c, ext, acc)) { ok = false; return {}; }
         int64_t jstride = 0;
         for (auto& t : acc.addr.terms) {
-            if (t.var != 1) continue;
+            if (t.var != kv) continue;
             if (t.div == 1 && (t.mod == 0 || t.mod % 8 == 0)) jstride += t.coef;
             else if (t.div % 8 != 0) { ok = false; return {}; }
         }
@@ -266,7 +287,7 @@ struct VecW {
         bufs.push_back(acc.buffer);
         dtypes.push_back(acc.dtype);
         std::string p = ptr + std::to_string(slot) + psfx;
-        std::string addr = acc.addr.render({nn, k0});
+        std::string addr = acc.addr.render(names());
         std::vector<std::string> out(8);
         auto one = [&](const std::string& idx) -> std::string {
             switch (acc.dtype) {
@@ -284,7 +305,7 @@ struct VecW {
         const char* comp[4] = {"x", "y", "z", "w"};
         if (jstride == 0) {
             for (auto& t : acc.addr.terms)
-                if (t.var == 1) uniform_div = std::gcd(uniform_div, t.div);
+                if (t.var == kv) uniform_div = std::gcd(uniform_div, t.div);
             std::string v = fresh("w");
             lc.line("const float " + v + " = " + one(base) + ";");
             return std::vector<std::string>(8, v);
@@ -440,6 +461,28 @@ bool render_weight_affine(const sanic_program_desc* d, int node, const std::vect
     dtypes = vw.dtypes;
     uniform_div = vw.uniform_div;
     return ok;
+}
+
+// One run of 8 of an elementwise leaf at coordinates `c` over named variables `vars`, the run
+// moving along variable `kv` from its value vars[kv] (a multiple of 8): 8 f32 expressions, loads
+// in `lc`, arithmetic in `dc`; plain (not non-temporal) loads through pointers named
+// rb<i><sfx> for the buffers `bufs` (dtypes `dtypes`), which the caller declares.
+std::vector<std::string> render_run(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
+                                    const std::vector<int64_t>& ext, const std::vector<std::string>& vars, int kv,
+                                    Code& lc, Code& dc, const std::string& sfx, std::vector<int>& bufs,
+                                    std::vector<int>& dtypes, bool& ok) {
+    VecW vw{d};
+    vw.stream = false;
+    vw.vars = vars;
+    vw.kv = kv;
+    vw.ptr = "rb";
+    vw.psfx = sfx;
+    vw.sfx = sfx;
+    auto vals = vw.render(lc, dc, node, c, ext);
+    ok = vw.ok;
+    bufs = vw.bufs;
+    dtypes = vw.dtypes;
+    return vals;
 }
 
 // ───────────────────────── gemv ───────────────────────────────────────────────────────────

@@ -46,6 +46,13 @@ bool match_row_cond(const sanic_program_desc* d, int node, int rank, int& dim, i
 // update of this step feeding that attention), or -1.
 int attn_absorber(const sanic_program_desc* d, int si);
 
+// One run of 8 of an elementwise leaf (see skeletons.cpp): loads in `lc` through pointers
+// rb<i><sfx> for `bufs`, arithmetic in `dc`.
+std::vector<std::string> render_run(const sanic_program_desc* d, int node, const std::vector<Sym>& c,
+                                    const std::vector<int64_t>& ext, const std::vector<std::string>& vars, int kv,
+                                    Code& lc, Code& dc, const std::string& sfx, std::vector<int>& bufs,
+                                    std::vector<int>& dtypes, bool& ok);
+
 bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out);
 bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out);
 bool lower_attn_decode(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out);

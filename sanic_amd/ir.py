@@ -377,6 +377,32 @@ def rope(x: Node, position: Node, inv_freq: Node) -> Node:
     return flatten(out, -2, -1)
 
 
+def rope_table(position: Node, inv_freq: Node) -> Node:
+    """The rotation rope() applies, as a [seq, 2, F] value: [s, 0, f] = cos(angle[s, f]),
+    [s, 1, f] = sin(angle[s, f]), angle[s, f] = position[s]·inv_freq[f] (nn.rs:171-194). It
+    depends on the row and the frequency only, so every head that shares the positions can read
+    one materialisation of it instead of evaluating cos and sin per element."""
+    seq, F = position.shape[0], inv_freq.shape[0]
+    angle = unsqueeze(map_(MUL, unsqueeze(position, 1), unsqueeze(inv_freq, 0)), 1)   # [seq, 1, F]
+    which = coordinate((seq, 2, F), 1)
+    return map_(WHERE, map_(LT, which, const(0.5)), map_(COS, angle), map_(SIN, angle))
+
+
+def rope_tabled(x: Node, table: Node) -> Node:
+    """rope() over x [..., seq, hd] with the rotation read from a rope_table [seq, 2, F]:
+    out = x·cos + flip(x, pair)·sign·sin, the same rotate-half form."""
+    hd = x.shape[-1]
+    F = hd // 2
+    seq = x.shape[-2]
+    xs = split(x, -1, 2, F)                                         # [..., seq, 2, F]
+    cos_t = reindex(table, (seq, 1, F), [(((1, 0),), 0), ((), 0), (((1, 2),), 0)])
+    sin_t = reindex(table, (seq, 1, F), [(((1, 0),), 0), ((), 1), (((1, 2),), 0)])
+    sign = unsqueeze(map_(SUB, map_(MUL, iota(2), const(2.0)), const(1.0)), 1)  # [2, 1]
+    rotated = map_(MUL, flip(xs, -2), sign)
+    out = map_(ADD, map_(MUL, xs, cos_t), map_(MUL, rotated, sin_t))
+    return flatten(out, -2, -1)
+
+
 def update_cache(cache: Node, current: Node, position: Node, seq_dim: int) -> Node:
     """where(idx < pos+1 and pos < idx+1, current, cache) (nn.rs:208-212)."""
     idx = coordinate(cache, seq_dim)

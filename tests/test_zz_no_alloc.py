@@ -68,7 +68,7 @@ def test_execute_static_matches_execute_twice_second_smaller(dev, case):
 
 def test_execute_static_refuses_programs_beyond_its_scratch(dev):
     """Intermediates larger than the static scratch: a clear error, nothing launched."""
-    big = configs.flash_prefill(64, 16, 4096)          # RoPE'd Q and K: 32 MiB + 8 MiB of intermediates
+    big = configs.flash_prefill(128, 64, 4096)         # RoPE'd K (32 MiB) and the rotation table (1 MiB)
     exe = dev.prepare(big)
     bufs = {b.name: dev.alloc(b.nbytes) for b in big.buffers if b.role != SCRATCH}
     with pytest.raises(SanicError) as e:
