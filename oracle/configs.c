@@ -237,6 +237,8 @@ static double rms_inv(const double* x, int n, double eps) {
 
 int64_t oracle_llama_step(oracle_llama* m, int64_t token, int64_t pos, double* logits,
                           int threads) {
+    /* the storage of a materialised intermediate: the boundary policy's width */
+#define BND(v) (m->boundary_bf16 ? oracle_round_bf16(v) : f32r(v))
     const int H = m->hidden, NH = m->heads, NKV = m->kv_heads, HD = m->head_dim, FF = m->ffn;
     const int F = HD / 2;
     double* x = (double*)malloc(sizeof(double) * H);
@@ -262,8 +264,8 @@ int64_t oracle_llama_step(oracle_llama* m, int64_t token, int64_t pos, double* l
         matvec_rows(u, m->wq[l], NH * HD, H, q, threads);
         matvec_rows(u, m->wk[l], NKV * HD, H, kk, threads);
         matvec_rows(u, m->wv[l], NKV * HD, H, vv, threads);
-        for (int i = 0; i < NH * HD; i++) q[i] = f32r(q[i] * r);
-        for (int i = 0; i < NKV * HD; i++) { kk[i] = f32r(kk[i] * r); vv[i] = f32r(vv[i] * r); }
+        for (int i = 0; i < NH * HD; i++) q[i] = BND(q[i] * r);
+        for (int i = 0; i < NKV * HD; i++) { kk[i] = BND(kk[i] * r); vv[i] = BND(vv[i] * r); }
         /* RoPE (llama3 schedule) on q and k at `pos`; in-place cache row writes in bf16
          * (update_cache, nn.rs:208-212; V stored transposed, llama3_2.rs:160-173) */
         oracle_rope(q, NH, 1, HD, pos, inv_freq);
@@ -293,23 +295,25 @@ int64_t oracle_llama_step(oracle_llama* m, int64_t token, int64_t pos, double* l
                 const uint16_t* vr = m->vcache[l] + ((int64_t)j * HD + d) * m->capacity;
                 double acc = 0.0;
                 for (int64_t t = 0; t <= pos; t++) acc += sc[t] * bf(vr[t]);
-                att[h * HD + d] = f32r(acc / lsum);
+                att[h * HD + d] = BND(acc / lsum);
             }
         }
         /* o projection + residual */
         matvec_rows(att, m->wo[l], H, NH * HD, o, threads);
-        for (int i = 0; i < H; i++) x[i] = f32r(x[i] + o[i]);
-        /* MLP: gate/up with fused RMSNorm, silu(gate)·up in the down projection's leaf */
+        for (int i = 0; i < H; i++) x[i] = BND(x[i] + o[i]);
+        /* MLP: gate/up with fused RMSNorm, silu(gate)·up in the down projection's leaf (as
+         * its own bf16 stage under the bf16 policy) */
         r = rms_inv(x, H, m->eps);
         for (int i = 0; i < H; i++) u[i] = x[i] * bf(m->mlp_norm[l][i]);
         matvec_rows(u, m->wg[l], FF, H, gt, threads);
         matvec_rows(u, m->wu[l], FF, H, up, threads);
         for (int i = 0; i < FF; i++) {
-            double g = f32r(gt[i] * r), uu = f32r(up[i] * r);
+            double g = BND(gt[i] * r), uu = BND(up[i] * r);
             u[i] = g * (1.0 / (1.0 + exp(-g))) * uu;
+            if (m->boundary_bf16) u[i] = oracle_round_bf16(u[i]);
         }
         matvec_rows(u, m->wd[l], H, FF, o, threads);
-        for (int i = 0; i < H; i++) x[i] = f32r(x[i] + o[i]);
+        for (int i = 0; i < H; i++) x[i] = BND(x[i] + o[i]);
     }
     /* final norm fused into the tied lm_head, logits stored f32, first argmax */
     double r = rms_inv(x, H, m->eps);
@@ -317,9 +321,10 @@ int64_t oracle_llama_step(oracle_llama* m, int64_t token, int64_t pos, double* l
     matvec_rows(u, m->embed, m->vocab, H, logits, threads);
     int64_t best = 0;
     for (int n = 0; n < m->vocab; n++) {
-        logits[n] = f32r(logits[n] * r);
+        logits[n] = BND(logits[n] * r);
         if (logits[n] > logits[best]) best = n;
     }
     free(x); free(u); free(q); free(kk); free(vv); free(att); free(o); free(gt); free(up); free(sc);
     return best;
+#undef BND
 }

@@ -91,6 +91,9 @@ typedef struct oracle_llama {
     const uint16_t* wd[32];                   /* [hidden, ffn]                          */
     uint16_t* kcache[32];                     /* [kv, capacity, hd] bf16                */
     uint16_t* vcache[32];                     /* [kv, hd, capacity] bf16 (transposed)   */
+    int boundary_bf16;                        /* 1: every materialised intermediate is
+                                               * stored bf16 (Policy { boundary: BF16 },
+                                               * cost.rs:16-27); 0: f32                   */
 } oracle_llama;
 
 /* One decode step at `pos` for `token`; writes logits [vocab] (f32-rounded values) and

@@ -160,7 +160,7 @@ def _split_heads(x, heads, hd):
 
 
 def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
-                 argmax_sched: Sched = None) -> Program:
+                 argmax_sched: Sched = None, boundary: int = ir.F32) -> Program:
     """One decode step of the Llama-3.2 graph (/root/reference/examples/llama3_2.rs:112-253),
     cut into the stages a carrier partition yields:
       embedding gather → per layer: q/k/v projections with the input RMSNorm fused into their
@@ -169,7 +169,10 @@ def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
       −∞ prefix mask of positions > pos) → o projection + residual (epilogue) → gate/up with
       the post-attention RMSNorm fused → silu(gate)·up (elementwise) → down projection +
       residual → final RMSNorm fused into the tied lm_head → argmax (key/tie carrier).
-    Intermediates are stored f32; weights and the K/V caches are bf16; `token` is u32."""
+    Weights and the K/V caches are bf16; `token` is u32. Every materialised intermediate is
+    stored in `boundary` — the reference's boundary-storage policy (`Policy { boundary }`,
+    /root/reference/src/cost.rs:16-27): f32 by default, bf16 as its `--bf16` run
+    (/root/reference/examples/llama3_2.rs:480-503); arithmetic stays f32 inside every stage."""
     S = shape
     H, hd, NH, NKV, F, V, Cap = S.hidden, S.head_dim, S.heads, S.kv_heads, S.ffn, S.vocab, S.capacity
     rep = NH // NKV
@@ -188,7 +191,8 @@ def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
         p.state(f"cache.{l}.value", (NKV, hd, Cap), ir.BF16)
     invf = ir.llama3_inv_freq(S.theta, hd // 2)
     emb = p.node("model.embed_tokens.weight")
-    x = p.pointwise("x.embed", ir.gather(emb, tokens, 0), ir.F32, role=3)      # [1, H]
+    B = boundary
+    x = p.pointwise("x.embed", ir.gather(emb, tokens, 0), B, role=3)      # [1, H]
     x = ir.reindex(x, (H,), [((), 0), (((1, 0),), 0)])                          # [H]
     for l in range(S.layers):
         pre = f"model.layers.{l}."
@@ -198,7 +202,7 @@ def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
             w = p.node(pre + f"self_attn.{nm}_proj.weight")
             proj[nm] = p.fused(f"{pre}{nm}", (rows,), H,
                                [(x, (STREAM,)), (g1, (STREAM,)), (w, (0, STREAM))],
-                               C.norm_fused_projection(H, S.eps), ir.F32, role=3)
+                               C.norm_fused_projection(H, S.eps), B, role=3)
         posn = p.node("position")
         # K cache row: rope(k) at `position` (update_cache along the cache sequence dim)
         kc = p.node(f"cache.{l}.key")
@@ -221,26 +225,26 @@ def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
         scores = ir.map_(ir.ADD, scores, mask)
         vexp = ir.permute(ir.expand_heads(p.node(f"cache.{l}.value"), 0, rep), (0, 2, 1))  # [NH, Cap, hd]
         att = p.fused(f"{pre}attn", (NH, hd), Cap, [(scores, (0, STREAM)), (vexp, (0, STREAM, 1))],
-                      C.online_softmax_weighted(), ir.F32, sched=attn_sched, role=3)
+                      C.online_softmax_weighted(), B, sched=attn_sched, role=3)
         attf = ir.flatten(att, 0, 1)                                            # [NH·hd]
         wo = p.node(pre + "self_attn.o_proj.weight")
         x = p.fused(f"{pre}x_attn", (H,), NH * hd, [(attf, (STREAM,)), (wo, (0, STREAM))], C.dot(2),
-                    ir.F32, epilogue=ir.map_(ir.ADD, x, ir.fold_value((H,))), role=3)
+                    B, epilogue=ir.map_(ir.ADD, x, ir.fold_value((H,))), role=3)
         g2 = p.node(pre + "post_attention_layernorm.weight")
         gu = {}
         for nm in ("gate", "up"):
             w = p.node(pre + f"mlp.{nm}_proj.weight")
             gu[nm] = p.fused(f"{pre}{nm}", (F,), H, [(x, (STREAM,)), (g2, (STREAM,)), (w, (0, STREAM))],
-                             C.norm_fused_projection(H, S.eps), ir.F32, role=3)
+                             C.norm_fused_projection(H, S.eps), B, role=3)
         # the SwiGLU cone as its own elementwise stage (a cut the partitioner makes so the
         # down projection's leaf is a plain load, not silu recomputed per output row)
-        hsw = p.pointwise(f"{pre}mlp.h", ir.map_(ir.MUL, ir.silu(gu["gate"]), gu["up"]), ir.F32, role=3)
+        hsw = p.pointwise(f"{pre}mlp.h", ir.map_(ir.MUL, ir.silu(gu["gate"]), gu["up"]), B, role=3)
         wd = p.node(pre + "mlp.down_proj.weight")
-        x = p.fused(f"{pre}x_mlp", (H,), F, [(hsw, (STREAM,)), (wd, (0, STREAM))], C.dot(2), ir.F32,
+        x = p.fused(f"{pre}x_mlp", (H,), F, [(hsw, (STREAM,)), (wd, (0, STREAM))], C.dot(2), B,
                     epilogue=ir.map_(ir.ADD, x, ir.fold_value((H,))), role=3)
     gf = p.node("model.norm.weight")
     logits = p.fused("logits", (V,), H, [(x, (STREAM,)), (gf, (STREAM,)), (emb, (0, STREAM))],
-                     C.norm_fused_projection(H, S.eps), ir.F32)
+                     C.norm_fused_projection(H, S.eps), B)
     p.fused("token", (1,), V, [(logits, (STREAM,)), (ir.iota(V), (STREAM,))], C.first_argmax(), ir.U32,
             sched=argmax_sched or Sched(lane_stream=True, waves=4, chunk=4, split=64))
     p.pointwise("position.next", ir.map_(ir.ADD, p.node("position"), ir.const(1.0)), ir.F32,

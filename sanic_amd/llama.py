@@ -1,5 +1,6 @@
 """Stateful decode over the HIP backend: the `Graph::compile_for` → `instantiate` →
-`Machine::step` path (/root/reference/src/graph.rs:231-345) for the Llama-3.2 decode program.
+`Machine::step` path (/root/reference/src/graph.rs:231-345) for the Llama-3.2 decode program,
+on the generic `sanic_amd.graph` machine.
 
 States (the K/V caches, the position and the current token) are allocated and zeroed at
 instantiation (graph.rs:297-310); one step is one hipGraph replay; the greedy token is written
@@ -17,29 +18,28 @@ import numpy as np
 
 from . import configs, ir
 from .backend import Buffer, HipDevice
-from .program import STATE
+from .graph import Graph
 
 
 class LlamaMachine:
     def __init__(self, dev: HipDevice, weights: Dict[str, Buffer],
                  shape: configs.LlamaShape = configs.LLAMA_1B, attn_sched=None,
-                 variants: Optional[Dict[int, int]] = None):
+                 variants: Optional[Dict[int, int]] = None, boundary: int = ir.F32):
         """`variants` (stage -> tiling variant) is what the measured tuner ships
-        (`sanic_amd.tune`); none = the analytic choice of every kernel."""
+        (`sanic_amd.tune`); none = the analytic choice of every kernel. `boundary` is the
+        storage of every materialised intermediate (the reference's `--bf16` policy)."""
         self.dev = dev
         self.shape = shape
-        self.prog = configs.llama_decode(shape, attn_sched=attn_sched)
-        if variants:
-            self.prog = self.prog.with_variants(variants)
-        self.exe = dev.prepare(self.prog)
-        self.bind: Dict[str, Buffer] = dict(weights)
-        for b in self.prog.buffers:
-            if b.role == STATE:
-                buf = dev.alloc(b.nbytes)
-                buf.upload(bytes(b.nbytes))          # states start at zero
-                self.bind[b.name] = buf
+        graph = Graph(configs.llama_decode(shape, attn_sched=attn_sched, boundary=boundary))
+        graph.output("logits")
+        graph.output("token")
+        self.step_program = graph.compile_for(dev, variants)
+        self.machine = self.step_program.instantiate(weights)
+        self.prog = self.step_program.program
+        self.exe = self.step_program.exe
+        self.bind = self.machine.bind
+        self.replay = self.machine.replay
         self.tokens = self.bind["tokens"]
-        self.replay = self.exe.capture(self.bind)
         self.logits = self.replay.buffer("logits")
         self.token = self.replay.buffer("token")
 
@@ -63,7 +63,7 @@ class LlamaMachine:
         """One decode step; `token` overrides the fed-back token (prefill). Returns GPU s."""
         if token is not None:
             self.set_token(token)
-        return self.replay.step()
+        return self.machine.step()
 
     def prefill(self, prompt: List[int]) -> int:
         """Token-by-token prefill; returns the greedy token after the last prompt token."""
@@ -73,13 +73,14 @@ class LlamaMachine:
 
     def decode(self, n: int) -> float:
         """n greedy steps back to back (each step's token feeds the next); GPU seconds."""
-        return self.replay.step_many(n)
+        return self.machine.step_many(n)
 
     def last_token(self) -> int:
         return int(np.frombuffer(self.token.download(4), np.uint32)[0])
 
     def last_logits(self) -> np.ndarray:
-        return np.frombuffer(self.logits.download(), np.float32).copy()
+        """The last step's logits as stored (f32, or bf16 under the bf16 policy), widened."""
+        return self.machine.read("logits").astype(np.float32 if self.prog.by_name["logits"].dtype == ir.F32 else np.float64)
 
     def cache(self, layer: int, which: str) -> np.ndarray:
         b = self.prog.by_name[f"cache.{layer}.{which}"]

@@ -29,13 +29,13 @@ class OracleLlama(ctypes.Structure):
                 ("theta", ctypes.c_double), ("embed", P), ("final_norm", P),
                 ("attn_norm", P * 32), ("mlp_norm", P * 32), ("wq", P * 32), ("wk", P * 32),
                 ("wv", P * 32), ("wo", P * 32), ("wg", P * 32), ("wu", P * 32), ("wd", P * 32),
-                ("kcache", P * 32), ("vcache", P * 32)]
+                ("kcache", P * 32), ("vcache", P * 32), ("boundary_bf16", ctypes.c_int)]
 
 
 class OracleModel:
     """oracle_llama_step (oracle/configs.c) over host weights; keeps its own K/V caches."""
 
-    def __init__(self, shape: configs.LlamaShape, w):
+    def __init__(self, shape: configs.LlamaShape, w, boundary_bf16: bool = False):
         self.shape = shape
         self.w = w
         S = shape
@@ -45,6 +45,7 @@ class OracleModel:
         m.layers, m.hidden, m.heads, m.kv_heads = S.layers, S.hidden, S.heads, S.kv_heads
         m.head_dim, m.ffn, m.vocab, m.capacity = S.head_dim, S.ffn, S.vocab, S.capacity
         m.eps, m.theta = S.eps, S.theta
+        m.boundary_bf16 = int(boundary_bf16)
         p = lambda a: a.ctypes.data
         m.embed = p(w["model.embed_tokens.weight"])
         m.final_norm = p(w["model.norm.weight"])

@@ -39,3 +39,26 @@ def test_llama_step_oracle_matches_interpreter_schedule():
             vc = (om.vc[l].astype(np.uint32) << 16).view(np.float32)
             np.testing.assert_array_equal(res[f"cache.{l}.key"].astype(np.float32), kc)
             np.testing.assert_array_equal(res[f"cache.{l}.value"].astype(np.float32), vc)
+
+
+def test_llama_step_oracle_bf16_boundary_matches_interpreter_schedule():
+    """The same pin under the reference's bf16 boundary policy (llama3_2.rs:480-503,
+    cost.rs:16-27): every intermediate of the schedule stored bf16, the fused loop rounding at
+    the same cuts."""
+    from sanic_amd import ir
+    w = synth_weights(TINY, seed=5)
+    prog = configs.llama_decode(TINY, boundary=ir.BF16)
+    om = OracleModel(TINY, w, boundary_bf16=True)
+    toks = [3, 17, 250, 9]
+    for pos, t in enumerate(toks):
+        vals = _values(prog, w, om.kc, om.vc, t, pos)
+        res = oracle.run_program(prog, vals)
+        tok_ref, logits_ref = om.step(t, pos)
+        # bf16-stored logits and caches: bit for bit at this size (measured), the strongest pin
+        np.testing.assert_array_equal(res["logits"], logits_ref)
+        assert int(res["token"][0]) == tok_ref
+        for l in range(TINY.layers):
+            kc = (om.kc[l].astype(np.uint32) << 16).view(np.float32)
+            vc = (om.vc[l].astype(np.uint32) << 16).view(np.float32)
+            np.testing.assert_array_equal(res[f"cache.{l}.key"].astype(np.float32), kc)
+            np.testing.assert_array_equal(res[f"cache.{l}.value"].astype(np.float32), vc)
