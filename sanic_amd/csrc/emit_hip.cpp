@@ -362,6 +362,10 @@ __device__ __forceinline__ float sanic_stride4_sum(float v) { // Î£ over lanes â
   v += sanic_dpp<0x128>(v);
   return sanic_rows_sum(v);
 }
+__device__ __forceinline__ float sanic_half_sum(float v) {   // Î£ over lanes i, i^32
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
 __device__ __forceinline__ float sanic_stride8_sum(float v) { // Î£ over lanes â‰¡ i (mod 8)
   return sanic_rows_sum(v + sanic_dpp<0x128>(v));
 }

@@ -1455,18 +1455,34 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     const sanic_stage& st = d->stages[si];
     const sanic_carrier& c = st.carrier;
     const int64_t N = P.N, K = P.K;
-    // Strip form: a workgroup owns 32 columns over the whole K, so no K slices meet across
-    // workgroups. The activation factors of every k (and the row slots) are computed once into
-    // LDS; lane l reads 8 columns (16 bytes) of row (l / 4) of each 16-row step, the 4 waves take
-    // a quarter of K each; lanes of one column group meet by shuffles, waves in LDS. Strips are
-    // dealt XCD-aware: workgroups b and b + 8 (one XCD) own adjacent strips, so the two halves of
-    // a 128-byte line are read through the same L2.
-    const int SW = 32;                            // strip width (columns); 64 measured slower
+    // Strip form: a workgroup owns SW columns over K / KSL rows. The activation factors of every k
+    // (and the row slots, over the whole K) are computed once into LDS; lane l reads 8 columns
+    // (16 bytes) of row (l / (SW/8)) of each row step, the 8 waves take an eighth of the slice
+    // each; lanes of one column group meet by shuffles, waves in LDS.
+    //   variant 0: 128-column strips (256 contiguous bytes per row) over four K slices; the slices
+    //     of a strip sit on one XCD (blockIdx b, b + 8, ...) and meet through scratch: the last
+    //     arrival adds them in slice order (deterministic) and finishes. B1 (2048 × 8192):
+    //     11.3 µs, against 12.3 for variant 1, 12.4 for 64 × 2 and 11.9 for 256 × 8 — longer
+    //     contiguous runs per row help; whole 128-byte lines alone (64 × 2) do not.
+    //   variant 1: 32-column strips over the whole K (no merge); workgroups b and b + 8 own
+    //     adjacent strips so the two halves of a 128-byte line are read through the same L2.
+    //   variants 2, 3: 64 / 256-column strips over 2 / 8 K slices.
+    static const int kStrip[][2] = {{128, 4}, {32, 1}, {64, 2}, {256, 8}};   // (columns, K slices)
+    const int kvar = st.sched.variant > 0 && st.sched.variant < 4 ? st.sched.variant : 0;
+    const int SW = kStrip[kvar][0];               // strip width (columns)
+    const int KSL = kStrip[kvar][1];              // K slices per strip
     const int NT = 512;                           // 8 waves: 16 row loads per lane
     const int LPR = SW / 8, RPS = 64 / LPR, NWV = NT / 64;   // lanes per row, rows per step, waves
-    if (N % (SW * 8) == 0 && K % (RPS * NWV) == 0 && K <= 8192) {
+    if (N % (SW * 8) == 0 && K % (RPS * NWV * KSL) == 0 && K <= 8192) {
         const int SC = (int)P.cslots.size(), SR = (int)P.rslots.size();
-        const int64_t NS = N / SW, KQ = K / NWV, IT = KQ / RPS;   // strips, rows per wave, row steps
+        const int64_t NS = N / SW, KH = K / KSL, KQ = KH / NWV, IT = KQ / RPS;   // strips, slice rows, rows per wave, row steps
+        int64_t part_off = 0, counter_off = 0;
+        if (KSL > 1) {
+            part_off = scratch;
+            scratch += ((KSL * SC * N * 4 + 255) / 256) * 256;
+            counter_off = scratch;
+            scratch += ((NS * 4 + 255) / 256) * 256;
+        }
         Renderer R(d);
         Code k;
         k.indent = 1;
@@ -1474,15 +1490,17 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("__shared__ __attribute__((aligned(16))) float red[" + std::to_string(NWV) + "][" + std::to_string(SC * SW) + "];");
         if (SR) k.line("__shared__ float rred[" + std::to_string(NWV) + "][" + std::to_string(SR) + "];");
         k.line("const int t = threadIdx.x, lane = t & 63, wv = t >> 6;");
-        k.line("const idx_t strip = (blockIdx.x % 8) * " + std::to_string(NS / 8) + " + blockIdx.x / 8;");
+        k.line("const idx_t strip = (blockIdx.x % 8) * " + std::to_string(NS / 8) + " + (blockIdx.x / 8) / " + std::to_string(KSL) + ";");
+        k.line("const idx_t slice = (blockIdx.x / 8) % " + std::to_string(KSL) + ";");
         k.line("const idx_t n0 = strip * " + std::to_string(SW) + " + (lane & " + std::to_string(LPR - 1) + ") * 8;");
+        const std::string krow0 = "(slice * " + std::to_string(KH) + " + (idx_t)wv * " + std::to_string(KQ) + ")";
         // weight loads first (every row step of this lane), then the LDS prologue
         std::vector<std::vector<std::string>> wv_(IT);
         Code wdc;
         wdc.indent = k.indent;
         for (int64_t i = 0; i < IT; i++) {
             VecW vw{d};
-            vw.nn = "((idx_t)wv * " + std::to_string(KQ) + " + " + std::to_string(i * RPS) + " + (lane / " + std::to_string(LPR) + "))";
+            vw.nn = "(" + krow0 + " + " + std::to_string(i * RPS) + " + (lane / " + std::to_string(LPR) + "))";
             vw.k0 = "n0";
             vw.ptr = "wb";
             vw.psfx = "";
@@ -1524,7 +1542,7 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         for (int cs = 0; cs < SC; cs++)
             for (int j = 0; j < 8; j++) k.line("float acc" + std::to_string(cs) + "_" + std::to_string(j) + " = 0.0f;");
         for (int64_t i = 0; i < IT; i++) {
-            const std::string kr = "((int)wv * " + std::to_string(KQ) + " + " + std::to_string(i * RPS) + " + (lane / " + std::to_string(LPR) + "))";
+            const std::string kr = "(int)(" + krow0 + " + " + std::to_string(i * RPS) + " + (lane / " + std::to_string(LPR) + "))";
             for (int cs = 0; cs < SC; cs++) {
                 const std::string f = "f" + std::to_string(cs) + "_" + std::to_string(i);
                 k.line("const float " + f + " = fl[" + std::to_string(cs) + "][" + kr + "];");
@@ -1538,7 +1556,7 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         for (int cs = 0; cs < SC; cs++)
             for (int j = 0; j < 8; j++) {
                 std::string a = "acc" + std::to_string(cs) + "_" + std::to_string(j);
-                k.line(a + " = " + (LPR == 4 ? "sanic_stride4_sum(" : "sanic_stride8_sum(") + a + ");");
+                k.line(a + " = " + (LPR == 4 ? "sanic_stride4_sum(" : LPR == 8 ? "sanic_stride8_sum(" : LPR == 16 ? "sanic_rows_sum(" : "sanic_half_sum(") + a + ");");
             }
         k.line("if (lane < " + std::to_string(LPR) + ") {");
         for (int cs = 0; cs < SC; cs++) {
@@ -1548,13 +1566,38 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         }
         k.line("}");
         k.line("__syncthreads();");
+        auto wave_sum_of = [&](int cs) {
+            std::string i = std::to_string(cs) + " * " + std::to_string(SW) + " + t", sum = "red[0][" + i + "]";
+            for (int w = 1; w < NWV; w++) sum = "(" + sum + " + red[" + std::to_string(w) + "][" + i + "])";
+            return sum;
+        };
+        if (KSL > 1) {
+            // this slice's column sums to scratch, then the later of the strip's workgroups
+            // finishes: the slices' partials added in slice order
+            k.line("if (t < " + std::to_string(SW) + ") {");
+            for (int cs = 0; cs < SC; cs++)
+                k.line("  sanic_st(a.scratch + " + std::to_string(part_off / 4) + " + (slice * " + std::to_string(SC) + " + " + std::to_string(cs) + ") * " +
+                       std::to_string(N) + " + strip * " + std::to_string(SW) + " + t, " + wave_sum_of(cs) + ");");
+            k.line("}");
+            k.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(counter_off) + ") + strip;");
+            emit_arrival(k, "sanic_last", "t", "cnt", std::to_string(KSL) + "u");
+            k.line("if (!sanic_last) return;");
+            k.line("if (t == 0) sanic_st(cnt, 0u);");
+        }
         k.line("if (t < " + std::to_string(SW) + ") {");
         k.indent++;
         k.line("const idx_t nn = strip * " + std::to_string(SW) + " + t;");
         std::string arr = "const float accq[" + std::to_string(std::max(SC, 1)) + "] = {";
         for (int cs = 0; cs < SC; cs++) {
-            std::string i = std::to_string(cs) + " * " + std::to_string(SW) + " + t", sum = "red[0][" + i + "]";
-            for (int w = 1; w < NWV; w++) sum = "(" + sum + " + red[" + std::to_string(w) + "][" + i + "])";
+            std::string sum;
+            if (KSL > 1) {
+                for (int q = 0; q < KSL; q++) {
+                    std::string pq = "sanic_ld(a.scratch + " + std::to_string(part_off / 4) + " + (" + std::to_string(q * SC + cs) + ") * " + std::to_string(N) + " + nn)";
+                    sum = q ? "(" + sum + " + " + pq + ")" : pq;
+                }
+            } else {
+                sum = wave_sum_of(cs);
+            }
             arr += std::string(cs ? ", " : "") + sum;
         }
         if (SC == 0) arr += "0.0f";
@@ -1572,11 +1615,14 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("}");
         const std::string kname = "sanic_gemvt_" + std::to_string(N) + "x" + std::to_string(K);
         std::ostringstream src;
-        src << kPrelude << R.args_struct({}) << "extern \"C\" __global__ void __launch_bounds__(" << NT << ") " << kname << "(Args a) {\n"
-            << R.entry() << k.str() << "}\n";
-        out.kernel_kind = "skeleton:gemv_kmajor[strips " + std::to_string(SW) + "]";
+        src << kPrelude << R.args_struct(KSL > 1 ? std::vector<std::string>{"float* __restrict__ scratch"} : std::vector<std::string>{})
+            << "extern \"C\" __global__ void __launch_bounds__(" << NT << ") " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
+        out.kernel_kind = "skeleton:gemv_kmajor[strips " + std::to_string(SW) + (KSL > 1 ? " x" + std::to_string(KSL) + " slices" : "") + "]";
         out.source = "// sched-strategy: max-memory-clause\n" + src.str();   // B1 12.26 → 12.07 µs
-        out.launches.push_back({kname, "", dim3((unsigned)NS), dim3((unsigned)NT), 0, R.arg_list()});
+        out.variants = 4;
+        std::vector<Arg> args = R.arg_list();
+        if (KSL > 1) args.push_back({Arg::SCRATCH, 0});
+        out.launches.push_back({kname, "", dim3((unsigned)(NS * KSL)), dim3((unsigned)NT), 0, args});
         return true;
     }
     if (N % 512 || K % 64) return false;

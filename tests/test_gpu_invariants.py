@@ -255,6 +255,19 @@ def test_soak_kslice_gemv(dev):
     assert exe.stage_kernel(0).startswith("skeleton:gemv_kmajor["), exe.stage_kernel(0)
 
 
+def test_soak_sliced_strip_gemv(dev):
+    """The K-major GEMV's 128-column strips over four K slices (the last workgroup of each strip
+    adds the slices in slice order): 5000 replays, bit-identical."""
+    K, N = 2048, 8192
+    prog = configs.rmsnorm_projection(M=1, K=K, N=N, kmajor=True)
+    wbits = oracle.synth_bf16(943, K * N, "normal", 0.0, 0.02)
+    vals = {"x": oracle.synth(941, K, dtype=ir.BF16).reshape(1, K),
+            "g": oracle.synth(942, K, "normal", 1.0, 0.02, dtype=ir.BF16),
+            "W": from_bf16_bits(wbits).astype(np.float64).reshape(K, N)}
+    exe = _soak(dev, prog, vals, "y")
+    assert "x4 slices" in exe.stage_kernel(0), exe.stage_kernel(0)
+
+
 def test_soak_flash_split_variant(dev):
     """The flash split variant (two workgroups per block exchange (m, ℓ, o) partials, the later
     one combines in a fixed operand order): 5000 replays, bit-identical."""

@@ -38,10 +38,13 @@ def test_b1_rmsnorm_gemv_rows_layout(dev, M):
     assert bf16_rel(got["y"], want) < 2e-2
 
 
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 @pytest.mark.parametrize("K,N", [(2048, 8192), (256, 1024)])
-def test_b1_rmsnorm_gemv_kmajor(dev, K, N):
-    """Config B1 as configured: W bf16 [K, N] (K-major), the N-contiguous gemv skeleton."""
-    prog = configs.rmsnorm_projection(M=1, K=K, N=N, kmajor=True)
+def test_b1_rmsnorm_gemv_kmajor(dev, K, N, variant):
+    """Config B1 as configured: W bf16 [K, N] (K-major), the N-contiguous gemv skeleton in every
+    strip form (0: 128 columns × 4 K slices meeting in scratch; 1: 32-column whole-K strips;
+    2: 64 × 2; 3: 256 × 8)."""
+    prog = configs.rmsnorm_projection(M=1, K=K, N=N, kmajor=True).with_variants({0: variant})
     x = _bf16_vals(111, K).reshape(1, K)
     g = _bf16_vals(112, K, 1.0, 0.02)
     wbits = oracle.synth_bf16(113, K * N, "normal", 0.0, 0.02).reshape(K, N)
