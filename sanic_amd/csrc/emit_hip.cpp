@@ -289,6 +289,33 @@ __device__ __forceinline__ unsigned short sanic_to_bf16(float v) {
   return (unsigned short)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
 }
 __device__ __forceinline__ float sanic_round_bf16(float v) { return sanic_bf16(sanic_to_bf16(v)); }
+// sin / cos of an f32 angle: Cody–Waite reduction by π/2 (Cody & Waite, "Software Manual for the
+// Elementary Functions", 1980) with π/2 split into 8 + 11 significant bits and an f32 tail, so
+// n·c1 and n·c2 are exact for |n| < 4096 (|a| < 6400), then the hardware sine / cosine of the
+// remainder (|r| ≤ π/4, in revolutions as v_sin/v_cos take them) and the quadrant. Outside that
+// range, and for non-finite angles, the library functions.
+__device__ __forceinline__ void sanic_sincos_red(float a, float& s, float& c, int& q) {
+  const float n = __builtin_rintf(a * 0.63661977236758134f);
+  float r = __builtin_fmaf(-n, 0x1.92p0f, a);
+  r = __builtin_fmaf(-n, 0x1.fb4p-12f, r);
+  r = __builtin_fmaf(-n, 0x1.4442d2p-24f, r);
+  const float t = r * 0.15915494309189535f;
+  s = __builtin_amdgcn_sinf(t);
+  c = __builtin_amdgcn_cosf(t);
+  q = (int)n & 3;
+}
+__device__ __forceinline__ float sanic_sin(float a) {
+  if (!(__builtin_fabsf(a) < 6400.0f)) return sinf(a);
+  float s, c; int q;
+  sanic_sincos_red(a, s, c, q);
+  return q == 0 ? s : q == 1 ? c : q == 2 ? -s : -c;
+}
+__device__ __forceinline__ float sanic_cos(float a) {
+  if (!(__builtin_fabsf(a) < 6400.0f)) return cosf(a);
+  float s, c; int q;
+  sanic_sincos_red(a, s, c, q);
+  return q == 0 ? c : q == 1 ? -s : q == 2 ? -c : s;
+}
 __device__ __forceinline__ unsigned sanic_to_u32(float v) {
   if (v >= 4294967040.0f) return 0xFFFFFFFFu;
   if (!(v > 0.0f)) return 0u;
@@ -423,8 +450,8 @@ std::string map_expr(int op, const std::string& a, const std::string& b, const s
     case SANIC_OP_LOG: return "(__builtin_amdgcn_logf(" + a + ") * 0.693147180559945309f)";
     case SANIC_OP_SQRT: return "__builtin_amdgcn_sqrtf(" + a + ")";
     case SANIC_OP_TANH: return "tanhf(" + a + ")";
-    case SANIC_OP_SIN: return "sinf(" + a + ")";
-    case SANIC_OP_COS: return "cosf(" + a + ")";
+    case SANIC_OP_SIN: return "sanic_sin(" + a + ")";
+    case SANIC_OP_COS: return "sanic_cos(" + a + ")";
     case SANIC_OP_WHERE: return "((" + a + " != 0.0f) ? " + b + " : " + c + ")";
     case SANIC_OP_ROUND_BF16: return "sanic_round_bf16(" + a + ")";
     case SANIC_OP_ROUND_F32: return "(" + a + ")";
