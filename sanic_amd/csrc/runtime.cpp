@@ -96,8 +96,14 @@ struct sanic_hip_replay {
     std::vector<std::pair<int, int>> feedback;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    // kMultiStep consecutive steps in one graph (built on the first step_many that can use it):
+    // back-to-back steps then pay one graph launch per kMultiStep steps instead of one each
+    hipGraph_t graph_n = nullptr;
+    hipGraphExec_t graph_n_exec = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     ~sanic_hip_replay() {
+        if (graph_n_exec) hipGraphExecDestroy(graph_n_exec);
+        if (graph_n) hipGraphDestroy(graph_n);
         if (graph_exec) hipGraphExecDestroy(graph_exec);
         if (graph) hipGraphDestroy(graph);
         if (ev0) hipEventDestroy(ev0);
@@ -607,6 +613,36 @@ int sanic_hip_execute_static(sanic_hip_exe* exe, sanic_hip_buffer* const* bindin
 
 uint64_t sanic_hip_device_allocations(void) { return g_device_allocations.load(std::memory_order_relaxed); }
 
+static const int kMultiStep = 8;
+
+// Capture `steps` consecutive steps (every stage, then the feedback conversions) into one graph.
+static void capture_steps(sanic_hip_replay* rp, int steps, hipGraph_t* graph, hipGraphExec_t* exec) {
+    sanic_hip_exe* exe = rp->exe;
+    hipStream_t s = exe->dev->stream;
+    SANIC_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    try {
+        for (int step = 0; step < steps; step++) {
+            enqueue(exe, rp->bound, rp->scratch->ptr());
+            for (auto& fb : rp->feedback) {
+                const auto& ob = exe->buffers[fb.first];
+                const auto& ib = exe->buffers[fb.second];
+                int64_t n = 1;
+                for (int k = 0; k < ob.rank; k++) n *= ob.shape[k];
+                hipLaunchKernelGGL(sanic_convert, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                                   (const void*)rp->bound[fb.first]->ptr(), ob.dtype, ob.scale,
+                                   (void*)rp->bound[fb.second]->ptr(), ib.dtype, ib.scale, n);
+            }
+        }
+    } catch (...) {
+        hipGraph_t g;
+        hipStreamEndCapture(s, &g);
+        if (g) hipGraphDestroy(g);
+        throw;
+    }
+    SANIC_HIP(hipStreamEndCapture(s, graph));
+    SANIC_HIP(hipGraphInstantiate(exec, *graph, nullptr, nullptr, 0));
+}
+
 int sanic_hip_capture(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int n_bindings, const int32_t* feedback,
                       int n_pairs, sanic_hip_replay** out) {
     return guarded([&] {
@@ -636,26 +672,7 @@ int sanic_hip_capture(sanic_hip_exe* exe, sanic_hip_buffer* const* bindings, int
             rp->feedback.push_back({o, i});
         }
         hipStream_t s = exe->dev->stream;
-        SANIC_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-        try {
-            enqueue(exe, rp->bound, rp->scratch->ptr());
-            for (auto& fb : rp->feedback) {
-                const auto& ob = exe->buffers[fb.first];
-                const auto& ib = exe->buffers[fb.second];
-                int64_t n = 1;
-                for (int k = 0; k < ob.rank; k++) n *= ob.shape[k];
-                hipLaunchKernelGGL(sanic_convert, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                                   (const void*)rp->bound[fb.first]->ptr(), ob.dtype, ob.scale,
-                                   (void*)rp->bound[fb.second]->ptr(), ib.dtype, ib.scale, n);
-            }
-        } catch (...) {
-            hipGraph_t g;
-            hipStreamEndCapture(s, &g);
-            if (g) hipGraphDestroy(g);
-            throw;
-        }
-        SANIC_HIP(hipStreamEndCapture(s, &rp->graph));
-        SANIC_HIP(hipGraphInstantiate(&rp->graph_exec, rp->graph, nullptr, nullptr, 0));
+        capture_steps(rp.get(), 1, &rp->graph, &rp->graph_exec);
         if (debug_level() >= 3) {
             int nl = 0;
             for (auto& st : exe->low.stages) nl += (int)st.launches.size();
@@ -725,8 +742,11 @@ int sanic_hip_step_many(sanic_hip_replay* rp, int n, double* gpu_seconds) {
             }
             SANIC_HIP(hipStreamSynchronize(s));
         }
+        const int many = (n - first) / kMultiStep;
+        if (many > 0 && !rp->graph_n_exec) capture_steps(rp, kMultiStep, &rp->graph_n, &rp->graph_n_exec);
         SANIC_HIP(hipEventRecord(rp->ev0, s));
-        for (int i = first; i < n; i++) SANIC_HIP(hipGraphLaunch(rp->graph_exec, s));
+        for (int i = 0; i < many; i++) SANIC_HIP(hipGraphLaunch(rp->graph_n_exec, s));
+        for (int i = first + many * kMultiStep; i < n; i++) SANIC_HIP(hipGraphLaunch(rp->graph_exec, s));
         SANIC_HIP(hipEventRecord(rp->ev1, s));
         SANIC_HIP(hipEventSynchronize(rp->ev1));
         float ms = 0;

@@ -112,3 +112,25 @@ def test_tiny_llama_bf16_boundary_policy_matches_oracle(dev):
     print("bf16 policy: logits max rel err", worst, "ties", ties)
     assert worst < 2e-2
     assert ties <= 2
+
+
+def test_back_to_back_steps_equal_single_steps(dev):
+    """decode(n) launches the multi-step graph (8 steps per launch) plus single steps; the
+    tokens, logits and caches equal those of n single-step replays bit for bit."""
+    w = synth_weights(TINY, seed=9)
+    bufs = {name: _upload(dev, a) for name, a in w.items()}
+    a = LlamaMachine(dev, bufs, TINY)
+    b = LlamaMachine(dev, bufs, TINY)
+    a.step(7)
+    b.step(7)
+    a.decode(10)                    # one 8-step graph + 2 single steps
+    toks = []
+    for _ in range(10):
+        b.step()
+        toks.append(b.last_token())
+    assert a.position() == b.position() == 11
+    assert a.last_token() == toks[-1]
+    assert np.array_equal(a.last_logits(), b.last_logits())
+    for l in range(TINY.layers):
+        for which in ("key", "value"):
+            assert np.array_equal(a.cache(l, which), b.cache(l, which))
