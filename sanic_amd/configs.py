@@ -163,8 +163,9 @@ def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
                  argmax_sched: Sched = None, boundary: int = ir.F32) -> Program:
     """One decode step of the Llama-3.2 graph (/root/reference/examples/llama3_2.rs:112-253),
     cut into the stages a carrier partition yields:
-      embedding gather → per layer: q/k/v projections with the input RMSNorm fused into their
-      folds (norm-fused carrier) → in-place K/V cache row writes (update_cache, RoPE on k) →
+      per layer: q/k/v projections with the input RMSNorm fused into their folds (norm-fused
+      carrier; layer 0 reads the embedding row through a gather in its leaves) → in-place K/V
+      cache row writes (update_cache, RoPE on k) →
       decode attention over the cache (online-softmax carrier; RoPE on q inside its leaf, the
       −∞ prefix mask of positions > pos) → o projection + residual (epilogue) → gate/up with
       the post-attention RMSNorm fused → silu(gate)·up (elementwise) → down projection +
@@ -192,8 +193,9 @@ def llama_decode(shape: LlamaShape = LLAMA_1B, attn_sched: Sched = None,
     invf = ir.llama3_inv_freq(S.theta, hd // 2)
     emb = p.node("model.embed_tokens.weight")
     B = boundary
-    x = p.pointwise("x.embed", ir.gather(emb, tokens, 0), B, role=3)      # [1, H]
-    x = ir.reindex(x, (H,), [((), 0), (((1, 0),), 0)])                          # [H]
+    # the embedding row is read where it is used (layer 0's q/k/v leaves and its residual): a
+    # gather is a load, so it is not materialised as a stage of its own
+    x = ir.reindex(ir.gather(emb, tokens, 0), (H,), [((), 0), (((1, 0),), 0)])   # [H]
     for l in range(S.layers):
         pre = f"model.layers.{l}."
         g1 = p.node(pre + "input_layernorm.weight")

@@ -235,6 +235,37 @@ struct VecW {
     std::vector<std::string> render(Code& lc, Code& dc, int node, const std::vector<Sym>& c, const std::vector<int64_t>& ext) {
         const sanic_node& n = d->nodes[node];
         if (n.kind == SANIC_NODE_CONST) return std::vector<std::string>(8, flit(n.value));
+        if (n.kind == SANIC_NODE_GATHER) {
+            // src[.., index(..), ..]: the index (rounded half away from zero and clamped, as the
+            // scalar renderer's gather) must be one value for the whole run; the gathered source
+            // dim becomes a run-invariant variable of its own
+            const sanic_node& src = d->nodes[n.in[0]];
+            const sanic_node& ix = d->nodes[n.in[1]];
+            std::vector<Sym> ic(c.begin() + n.dim, c.begin() + n.dim + ix.rank);
+            std::vector<std::string> iv = render(lc, dc, n.in[1], ic, ext);
+            if (!ok) return {};
+            for (auto& v : iv) if (v != iv[0]) { ok = false; return {}; }
+            // the index value is needed for addressing, so its arithmetic goes with the loads
+            Code tmp;
+            tmp.indent = lc.indent;
+            tmp.s << dc.str();
+            dc.s.str("");
+            const std::string gi = fresh("gi");
+            lc.s << tmp.str();
+            lc.line("idx_t " + gi + " = (idx_t)roundf(" + iv[0] + ");");
+            lc.line(gi + " = " + gi + " < 0 ? 0 : (" + gi + " > " + std::to_string(src.shape[n.dim] - 1) + " ? " +
+                    std::to_string(src.shape[n.dim] - 1) + " : " + gi + ");");
+            if (vars.empty()) vars = {nn, k0};
+            const int gv = (int)vars.size();
+            vars.push_back(gi);
+            std::vector<int64_t> ext2 = ext;
+            ext2.resize(gv + 1, 1);
+            ext2[gv] = src.shape[n.dim];
+            std::vector<Sym> sc(src.rank);
+            for (int j = 0; j < src.rank; j++)
+                sc[j] = j < n.dim ? c[j] : j == n.dim ? Sym::var(gv) : c[j - 1 + ix.rank];
+            return render(lc, dc, n.in[0], sc, ext2);
+        }
         if (n.kind == SANIC_NODE_IOTA || n.kind == SANIC_NODE_COORDINATE) {
             // the coordinate's own value: one value per run when it does not move within an
             // aligned run of 8, else base + j·coef when it moves by a constant step

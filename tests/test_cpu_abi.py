@@ -59,10 +59,10 @@ def test_lowering_chooses_the_expected_kernel(name):
         "D2": (configs.int4_matmul(M=128), 0, "skeleton:gemm[128x32,grp,"),
         "C1": (configs.flash_prefill(), 2, "skeleton:flash_prefill"),
         # q/k/v batched into one launch; this step's K/V cache writes done by the attention kernel
-        "E_qkv": (configs.llama_decode(), 1, "skeleton:gemv[batched 3]"),
-        "E_attn": (configs.llama_decode(), 6, "skeleton:attn_decode[rep 4]+writes2"),
+        "E_qkv": (configs.llama_decode(), 0, "skeleton:gemv[batched 3]"),
+        "E_attn": (configs.llama_decode(), 5, "skeleton:attn_decode[rep 4]+writes2"),
         # gate/up batched with silu(gate)·up computed per row pair
-        "E_gateup": (configs.llama_decode(), 8, "skeleton:gemv[batched 2]+paired"),
+        "E_gateup": (configs.llama_decode(), 7, "skeleton:gemv[batched 2]+paired"),
     }
     p, stage, want = progs[name]
     kind, src = p.emit(stage)
@@ -76,11 +76,11 @@ def test_lowering_chooses_the_expected_kernel(name):
     ("D1", lambda: configs.int4_matmul(), 0, "iterative-ilp"),
     ("B1", lambda: configs.rmsnorm_projection(kmajor=True), 0, "max-memory-clause"),
     ("B1_rows", lambda: configs.rmsnorm_projection(kmajor=False), 0, "max-memory-clause"),
-    ("E_gateup", lambda: configs.llama_decode(), 8, "max-memory-clause"),
-    ("E_down", lambda: configs.llama_decode(), 11, "iterative-ilp"),
-    ("E_o", lambda: configs.llama_decode(), 7, None),
-    ("E_qkv", lambda: configs.llama_decode(), 1, None),
-    ("E_lm_head", lambda: configs.llama_decode(), 177, "max-memory-clause"),
+    ("E_gateup", lambda: configs.llama_decode(), 7, "max-memory-clause"),
+    ("E_down", lambda: configs.llama_decode(), 10, "iterative-ilp"),
+    ("E_o", lambda: configs.llama_decode(), 6, None),
+    ("E_qkv", lambda: configs.llama_decode(), 0, None),
+    ("E_lm_head", lambda: configs.llama_decode(), 176, "max-memory-clause"),
     ("B2", lambda: configs.rmsnorm_projection(M=512), 0, None),
     ("C1", lambda: configs.flash_prefill(), 2, None),
     ("A", lambda: configs.direct_attention(), 0, None),
