@@ -504,8 +504,6 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
                 const std::vector<std::string> vars = {"hh", "(idx_t)0", "((idx_t)lq * 8 + " + std::to_string(ds * 32) + ")",
                                                        "(q0 + " + std::to_string(qt * 16) + " + l16)"};
                 std::vector<int> bufs, dts;
-                Code pl;
-                pl.indent = q_lc.indent;
                 q_vals[qt][ds] = render_run(d, P.qnode, P.qcoords, {NH, T, HD, NQ}, vars, 2, q_lc, q_dc, sfx, bufs, dts, ok);
                 for (size_t b = 0; b < bufs.size() && ok; b++)
                     k.line("const " + std::string(ctype_of(dts[b])) + "* __restrict__ rb" + std::to_string(b) + sfx + " = " + R.param(bufs[b]) + ";");

@@ -9,6 +9,8 @@ agreement with the interpreter running the whole decode schedule is pinned in
 tests/test_cpu_llama_oracle.py. Run from the repository root:
 
     python tests/golden/make_llama_e.py          # ≈25 min on 8 cores
+    python tests/golden/make_llama_e.py --bf16   # the same under the bf16 boundary policy
+                                                 # → llama_e_bf16.npz
 
 Contents (all arrays; no pickles):
   prompt [2048] i32, ids [2080] i32 (the argmax after every step, prompt and decode),
@@ -51,11 +53,11 @@ def check_steps():
     return np.array(s, np.int32)
 
 
-def main(out=os.path.join(os.path.dirname(os.path.abspath(__file__)), "llama_e.npz")):
+def main(out=os.path.join(os.path.dirname(os.path.abspath(__file__)), "llama_e.npz"), boundary_bf16=False):
     S = shape()
     t0 = time.time()
     w = synth_weights(S, seed=WEIGHT_SEED)
-    om = OracleModel(S, w)
+    om = OracleModel(S, w, boundary_bf16=boundary_bf16)
     prompt = prompt_ids(S.vocab)
     probe = np.random.default_rng(7).choice(S.vocab, 64, replace=False).astype(np.int32)
     steps = set(check_steps().tolist())
@@ -87,4 +89,8 @@ def main(out=os.path.join(os.path.dirname(os.path.abspath(__file__)), "llama_e.n
 
 
 if __name__ == "__main__":
-    main()
+    if "--bf16" in sys.argv:
+        # the reference's bf16 boundary policy (llama3_2.rs --bf16): every intermediate stored bf16
+        main(os.path.join(os.path.dirname(os.path.abspath(__file__)), "llama_e_bf16.npz"), boundary_bf16=True)
+    else:
+        main()

@@ -101,3 +101,28 @@ def test_device_specs_carry_the_cost_model_fields(dev):
     assert s.launch_overhead_s == 2.6e-6 and s.min_blocks == 2 * s.compute_units
     # Little's law at these figures: the decode GEMV's 33.5 MB in flight saturates HBM
     assert 33.5e6 / (s.hbm_bytes_per_s * s.mem_latency_s) >= 1.0
+
+
+@pytest.mark.parametrize("index", [0.0, 299.0, 150.5, 7.4])
+def test_gemv_reads_its_activation_through_a_gather(dev, index):
+    """The GEMV's activation leaf a gathered row (the decode step's layer 0 reading embed[token]
+    with no stage of its own): the index rounded half away from zero, as the interpreter's
+    gather (interp.rs, llround); norm-fused, against the oracle running the same program."""
+    from sanic_amd import carrier as C
+    from sanic_amd.program import STREAM, Program
+    V, K, N = 300, 2048, 512
+    p = Program()
+    emb = p.input("E", (V, K), ir.BF16)
+    idx = p.input("idx", (1,), ir.F32)
+    g = p.input("g", (K,), ir.BF16)
+    w = p.input("W", (N, K), ir.BF16)
+    x = ir.reindex(ir.gather(emb, idx, 0), (K,), [((), 0), (((1, 0),), 0)])
+    p.fused("y", (N,), K, [(x, (STREAM,)), (g, (STREAM,)), (w, (0, STREAM))], C.norm_fused_projection(K, 1e-5), ir.F32)
+    vals = {"E": _bf16_vals(131, V * K).reshape(V, K), "idx": np.array([index]),
+            "g": _bf16_vals(132, K, 1.0, 0.02), "W": _bf16_vals(133, N * K, 0.0, 0.02).reshape(N, K)}
+    got, exe = run_on_gpu(dev, p, vals)
+    want = oracle.run_program(p, vals)["y"]
+    err = float(np.max(np.abs(got["y"] - want) / (1 + np.abs(want))))
+    print(exe.stage_kernel(0), index, err)
+    assert exe.stage_kernel(0).startswith("skeleton:gemv")
+    assert err < 1e-4
