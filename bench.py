@@ -25,6 +25,12 @@ sys.path.insert(0, ROOT)
 
 PROMPT = 2048
 HBM_PEAK = 8.0e12
+# Boundary-storage policy of the timed decode step: f32 intermediates (the reference's default
+# `Policy`), whose greedy ids match the oracle's exactly; `--bf16-boundary` runs the reference's
+# `--bf16` policy (/root/reference/examples/llama3_2.rs:480-503), every materialised
+# intermediate stored bf16 — 0.9% faster, but its bf16 logits tie or swap the top two against an
+# f64 oracle on ≈5% of steps.
+BOUNDARY_BF16 = False
 
 
 def log(*a):
@@ -48,7 +54,7 @@ def device_weights(dev, shape, seed=1234):
     return bufs, keep
 
 
-def dominant_kernel_roofline(dev, shape, weights, reps=40, copies=8):
+def dominant_kernel_roofline(dev, shape, weights, reps=40, copies=8, boundary=None):
     """The decode step's dominant kernel — the batched gate/up RMSNorm-fused GEMV with the
     SwiGLU product computed per row pair (one launch: N = 2·ffn rows, K = hidden) — `copies`
     launches per hipGraph replay, copy r on layer r's weights (8 × 67 MB overflows the 256 MB
@@ -59,18 +65,20 @@ def dominant_kernel_roofline(dev, shape, weights, reps=40, copies=8):
     from sanic_amd import ir
     from sanic_amd.program import STREAM, Program
     H, F = shape.hidden, shape.ffn
+    B = boundary if boundary is not None else (ir.BF16 if BOUNDARY_BF16 else ir.F32)
+    bb = 2 if B == ir.BF16 else 4
     p = Program()
-    x = p.input("x", (H,), ir.F32)
+    x = p.input("x", (H,), B)
     for r in range(copies):
         g = p.input(f"g{r}", (H,), ir.BF16)
         ws = {nm: p.input(f"W{nm}{r}", (F, H), ir.BF16) for nm in ("gate", "up")}
         gu = {nm: p.fused(f"{nm}{r}", (F,), H, [(x, (STREAM,)), (g, (STREAM,)), (ws[nm], (0, STREAM))],
-                          C.norm_fused_projection(H, shape.eps), ir.F32) for nm in ("gate", "up")}
-        p.pointwise(f"h{r}", ir.map_(ir.MUL, ir.silu(gu["gate"]), gu["up"]), ir.F32)
+                          C.norm_fused_projection(H, shape.eps), B) for nm in ("gate", "up")}
+        p.pointwise(f"h{r}", ir.map_(ir.MUL, ir.silu(gu["gate"]), gu["up"]), B)
     exe = dev.prepare(p)
     kname = exe.stage_kernel(0)
     assert kname.startswith("skeleton:gemv[batched 2]+paired"), kname
-    xb = dev.from_values([0.5] * H, ir.F32)
+    xb = dev.from_values([0.5] * H, B)
     binds = {"x": xb}
     for r in range(copies):
         pre = f"model.layers.{r % shape.layers}."
@@ -79,8 +87,8 @@ def dominant_kernel_roofline(dev, shape, weights, reps=40, copies=8):
     rp = exe.capture(binds)
     rp.step_many(5)
     secs = rp.step_many(reps) / (reps * copies)
-    # weights + x (f32) + gain (bf16) + gate, up and h outputs (f32)
-    nbytes = 2 * F * H * 2 + H * 4 + H * 2 + 3 * F * 4
+    # weights + x + gain (bf16) + gate, up and h outputs (x and the outputs in the boundary dtype)
+    nbytes = 2 * F * H * 2 + H * bb + H * 2 + 3 * F * bb
     return {"bound": "hbm", "achieved": nbytes / secs / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": nbytes / secs / HBM_PEAK, "traffic": traffic_from_profile(),
             "kernel": f"sanic_gemv_{2 * F}x{H} ({kname})", "bytes_per_launch": nbytes,
@@ -114,7 +122,7 @@ def cpu_baseline(shape, seconds_budget=24.0):
     from tests.llama_ref import OracleModel, synth_weights
     threads = oracle.threads()
     w = synth_weights(shape, seed=99)
-    om = OracleModel(shape, w)
+    om = OracleModel(shape, w, boundary_bf16=BOUNDARY_BF16)
 
     def timed(nthreads, budget, max_steps):
         n, t0, tok = 0, time.perf_counter(), 1
@@ -129,7 +137,7 @@ def cpu_baseline(shape, seconds_budget=24.0):
     n1, el1 = timed(1, seconds_budget / 3, 4)
     # the interpreter leg: one layer (same widths, vocabulary 16384), one step
     one = configs.LlamaShape(layers=1, capacity=PROMPT + 1, vocab=16384)
-    prog = configs.llama_decode(one)
+    prog = configs.llama_decode(one, boundary=ir.BF16 if BOUNDARY_BF16 else ir.F32)
     vals = {name: (w[name].reshape(-1)[:int(np.prod(shp))].astype(np.uint32) << 16).view(np.float32)
             .astype(np.float64).reshape(shp) for name, shp in one.weight_shapes()}
     vals["tokens"] = np.array([1.0])
@@ -341,6 +349,8 @@ def main():
     ap.add_argument("--tune", action="store_true",
                     help="run the measured tiling tuner (SANIC_TUNE) on the decode program first and "
                          "bench the tuned program (tuning is outside the timed region)")
+    ap.add_argument("--bf16-boundary", action="store_true",
+                    help="store the decode step's intermediates bf16 (the reference's --bf16 policy)")
     ap.add_argument("--config", default=None, help="measure a secondary configuration instead: " + ", ".join(CONFIGS))
     args = ap.parse_args()
     if args.pmc_probe:
@@ -360,8 +370,10 @@ def main():
     import torch
     from sanic_amd import configs
     from sanic_amd.backend import HipDevice
+    from sanic_amd import ir
     from sanic_amd.llama import LlamaMachine
 
+    boundary = ir.BF16 if args.bf16_boundary or BOUNDARY_BF16 else ir.F32
     cap = PROMPT + max(32, args.steps, args.warmup)
     shape = configs.LlamaShape(capacity=cap)
     torch.cuda.init()
@@ -371,7 +383,7 @@ def main():
     tuned = None
     if args.tune:
         from sanic_amd import tune as tuner
-        prog = configs.llama_decode(shape)
+        prog = configs.llama_decode(shape, boundary=boundary)
         # zeroed bindings, the decode position rewound to the end of the prompt before every
         # timing: every candidate is judged on the same steps the bench times
         bind = tuner.zero_bindings(dev, prog)
@@ -383,9 +395,9 @@ def main():
             f"shipped {rep.shipped} {rep.choices}")
         tuned = {"shipped": rep.shipped, "choices": rep.choices,
                  "analytic_us": rep.baseline_s * 1e6, "tuned_us": rep.tuned_s * 1e6}
-        m = LlamaMachine(dev, weights, shape, variants=rep.variants)
+        m = LlamaMachine(dev, weights, shape, variants=rep.variants, boundary=boundary)
     else:
-        m = LlamaMachine(dev, weights, shape)
+        m = LlamaMachine(dev, weights, shape, boundary=boundary)
     log(f"prepared in {time.perf_counter() - t0:.1f}s")
 
     import numpy as np
@@ -413,7 +425,7 @@ def main():
 
     kv_bytes = sum(32768 * (p + 1) for p in range(PROMPT, PROMPT + args.steps)) / args.steps
     step_bytes = shape.weight_bytes() + kv_bytes
-    roof = dominant_kernel_roofline(dev, shape, weights)
+    roof = dominant_kernel_roofline(dev, shape, weights, boundary=boundary)
     step_roof = {"bytes_per_step": step_bytes, "achieved_GBps": step_bytes / (ms * 1e-3) / 1e9,
                  "frac_of_8TBps": step_bytes / (ms * 1e-3) / HBM_PEAK}
     rows = {}
@@ -427,7 +439,9 @@ def main():
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,0.02) bf16 weights, random prompt ids)",
-        "config": {"workload": "llama3.2-1b-shape decode, 2048-token prompt prefilled token-by-token, "
+        "config": {"workload": "llama3.2-1b-shape decode, "
+                               + ("bf16 boundary storage (the reference's --bf16 policy), " if boundary == ir.BF16 else "f32 intermediates, ")
+                               + "2048-token prompt prefilled token-by-token, "
                                f"greedy steps at positions {PROMPT}..{PROMPT + args.steps - 1}",
                    "global_batch": 1, "seq_len": PROMPT, "parallelism": "single-gpu"},
         "roofline": roof, "step_roofline": step_roof, "cpu_baseline": cpu, "configs": rows,
