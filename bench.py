@@ -106,7 +106,7 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(shape, seconds_budget=24.0):
+def cpu_baseline(shape, boundary_bf16, seconds_budget=24.0, interpreter=True):
     """The CPU path on this host, three legs, all outside the GPU's timed region:
       - the oracle's fused f64 decode step (oracle_llama_step: the rustgen-shaped loops over the
         bf16 weights) at positions 2048.. with every thread the host offers us (`value`),
@@ -118,11 +118,11 @@ def cpu_baseline(shape, seconds_budget=24.0):
     real step's (every weight read once, attention over p + 1 positions); only the time is used."""
     import numpy as np
     import oracle
-    from sanic_amd import configs
+    from sanic_amd import configs, ir
     from tests.llama_ref import OracleModel, synth_weights
     threads = oracle.threads()
     w = synth_weights(shape, seed=99)
-    om = OracleModel(shape, w, boundary_bf16=BOUNDARY_BF16)
+    om = OracleModel(shape, w, boundary_bf16=boundary_bf16)
 
     def timed(nthreads, budget, max_steps):
         n, t0, tok = 0, time.perf_counter(), 1
@@ -135,16 +135,18 @@ def cpu_baseline(shape, seconds_budget=24.0):
 
     n, el = timed(threads, seconds_budget / 3, 8)
     n1, el1 = timed(1, seconds_budget / 3, 4)
-    # the interpreter leg: one layer (same widths, vocabulary 16384), one step
+    # the interpreter leg: one layer (same widths, vocabulary 16384), one step (`interpreter`
+    # False leaves it out: the leg alone takes tens of seconds)
     one = configs.LlamaShape(layers=1, capacity=PROMPT + 1, vocab=16384)
-    prog = configs.llama_decode(one, boundary=ir.BF16 if BOUNDARY_BF16 else ir.F32)
+    prog = configs.llama_decode(one, boundary=ir.BF16 if boundary_bf16 else ir.F32)
     vals = {name: (w[name].reshape(-1)[:int(np.prod(shp))].astype(np.uint32) << 16).view(np.float32)
             .astype(np.float64).reshape(shp) for name, shp in one.weight_shapes()}
     vals["tokens"] = np.array([1.0])
     vals["position"] = np.array(float(PROMPT))
     t0 = time.perf_counter()
-    oracle.run_program(prog, vals)
-    el_i = time.perf_counter() - t0
+    if interpreter:
+        oracle.run_program(prog, vals)
+    el_i = time.perf_counter() - t0 if interpreter else None
     del om, w, vals
     return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{n} decode steps of the full model at positions {PROMPT}..{PROMPT + n - 1} "
@@ -433,7 +435,7 @@ def main():
         for name in CONFIGS:
             rows[name] = config_row(dev, name)[0]
             log(f"{name}: {rows[name]['kernel']} {rows[name]['us_per_launch']:.2f} us/launch, frac {rows[name]['frac']:.3f}")
-    cpu = None if args.no_cpu else cpu_baseline(shape)
+    cpu = None if args.no_cpu else cpu_baseline(shape, boundary == ir.BF16)
     out = {
         "metric": "tok/s Llama-3.2-1B-shape bf16 decode", "value": tok_s, "unit": "tok/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,

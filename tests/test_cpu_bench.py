@@ -22,3 +22,13 @@ def test_bench_defines_every_leg():
 def test_traffic_summary_is_parsed():
     t = _bench().traffic_from_profile()
     assert t is not None and 6.0e7 < t < 8.0e7
+
+
+def test_cpu_baseline_runs_under_both_policies():
+    """The CPU leg of the default bench run, on a one-layer model, under both storage policies."""
+    b = _bench()
+    from sanic_amd import configs
+    shape = configs.LlamaShape(layers=1, capacity=b.PROMPT + 8, vocab=16384)
+    for bf16 in (False, True):
+        r = b.cpu_baseline(shape, bf16, seconds_budget=0.3, interpreter=False)
+        assert r["value"] > 0 and r["kind"] == "port" and r["cores"] >= 1
