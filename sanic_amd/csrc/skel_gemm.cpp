@@ -165,7 +165,7 @@ bool render_weight_affine(const sanic_program_desc* d, int node, const std::vect
                           const std::vector<int64_t>& ext, Code& lc, Code& dc, const std::string& nn,
                           const std::string& k0, const std::string& sfx, std::vector<int>& bufs,
                           std::vector<int>& dtypes, std::vector<std::string>& q, std::string& A, std::string& B,
-                          bool& negB, int64_t& uniform_div, bool stream);
+                          bool& negB, int64_t& uniform_div, bool stream, bool raw_loads = false);
 
 bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredStage& out) {
     GemmPlan P;
@@ -289,8 +289,11 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     // grouped tiles: tiling variants {8 waves, load depth 4; 4 waves, depth 4; 8 waves, depth 2}
     const int gvar = grouped && st.sched.variant > 0 && st.sched.variant < 3 ? st.sched.variant : 0;
     if (grouped && BM == 128 && BN == 32 && gvar != 1) NTH = 512;
-    const int WGM = NTH / 128;                // waves along m (2 along n)
-    const int WM = BM / WGM, WN = BN / 2;     // per-wave tile
+    // waves along m and n: 4 × 2 / 2 × 2; grouped 32-column tiles of 8 waves 8 × 1, so no two
+    // waves form the same rows' Σ x
+    const int WGN = (grouped && NTH == 512 && BN == 32 && BM == 128) ? 1 : 2;
+    const int WGM = NTH / 64 / WGN;
+    const int WM = BM / WGM, WN = BN / WGN;   // per-wave tile
     const int MT = WM / 16, NT = WN / 16;
     // threads that load the B tile (all of them unless the tile has fewer runs of 8)
     const int BTH = std::min(NTH, BN * 8);
@@ -377,7 +380,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     k.line("const int l16 = lane & 15, lq = lane >> 4;");
     k.line("const idx_t nb = blockIdx.x % " + std::to_string(N / BN) + ", mb = blockIdx.x / " + std::to_string(N / BN) + ";");
     k.line("const idx_t m0 = mb * " + std::to_string(BM) + ", n0 = nb * " + std::to_string(BN) + ";");
-    k.line("const int wm = (wv >> 1) * " + std::to_string(WM) + ", wn = (wv & 1) * " + std::to_string(WN) + ";");
+    k.line("const int wm = (wv / " + std::to_string(WGN) + ") * " + std::to_string(WM) + ", wn = (wv % " + std::to_string(WGN) + ") * " + std::to_string(WN) + ";");
     k.line("f32x4 acc[" + std::to_string(MT) + "][" + std::to_string(NT) + "];");
     k.line("#pragma unroll");
     k.line("for (int i = 0; i < " + std::to_string(MT) + "; ++i)");
@@ -447,19 +450,17 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             Code l1, d1;
             l1.indent = d1.indent = c2.indent;
             if (grouped) {
-                // q as exact bf16 integers; this row's group s and z for the lanes' fold
+                // the loads only (q's packed word, the group's s and z as stored): the words
+                // are what a load set holds across the loop, and emit_stores widens them (so
+                // the back edge never waits for a load issued in the same iteration)
                 std::vector<std::string> qv;
                 std::string A_, B_;
                 bool nb = false;
                 int64_t ud = 0;
-                render_weight_affine(d, st.leaf[P.w], cw, {N, K}, l1, d1, nn, kk, "_b" + rs + sfx, rb, rd, qv, A_, B_, nb, ud, false);
+                render_weight_affine(d, st.leaf[P.w], cw, {N, K}, l1, d1, nn, kk, "_b" + rs + sfx, rb, rd, qv, A_, B_, nb, ud, false, true);
                 for (size_t b = 0; b < rb.size(); b++)
                     c2.line("const " + std::string(ctype_of(rd[b])) + "* __restrict__ wb" + std::to_string(b) + "_b" + rs + sfx + " = " + R.param(rb[b]) + ";");
-                c2.s << l1.str() << d1.str();
-                c2.line("const sanic_u32x4 rb" + rs + sfx + " = (sanic_u32x4){pk_bf16(" + qv[0] + ", " + qv[1] + "), pk_bf16(" + qv[2] + ", " +
-                        qv[3] + "), pk_bf16(" + qv[4] + ", " + qv[5] + "), pk_bf16(" + qv[6] + ", " + qv[7] + ")};");
-                c2.line("const float gs" + rs + sfx + " = " + A_ + ";");
-                c2.line("const float gz" + rs + sfx + " = " + (B_.empty() ? std::string("0.0f") : (nb ? "-" : "") + B_) + ";");
+                c2.s << l1.str();
                 continue;
             }
             auto vals = bkn ? render_weight_run(d, st.leaf[P.w], cwt, {K, N}, l1, d1, kk, nn, "_b" + rs + sfx, rb, rd, rok, rc, rr, false)
@@ -548,10 +549,28 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
                 col = "(((" + btid + " / " + std::to_string(BN) + ") + " + std::to_string(r * (BTH / BN)) + ") * 8)";
             }
             const std::string boff = bkn ? row + " * " + std::to_string(stride) + " + " + col : koff(row, col, stride);
+            if (grouped) {
+                // q as exact bf16 integers; this row's group s and z for the lanes' fold (the
+                // same rendering as emit_loads', whose loaded words these expressions read)
+                std::vector<std::string> qv;
+                std::string A_, B_;
+                bool nb = false;
+                int64_t ud = 0;
+                std::vector<int> gb, gd;
+                Code l1, d1;
+                l1.indent = d1.indent = c2.indent;
+                render_weight_affine(d, st.leaf[P.w], cw, {N, K}, l1, d1, "nn", "k0", "_b" + rs + sfx, gb, gd, qv, A_, B_, nb, ud, false, true);
+                c2.line("{");
+                c2.s << d1.str();
+                c2.line("*(sanic_u32x4*)(&b_lds[" + buf + "][" + boff + "]) = (sanic_u32x4){pk_bf16(" + qv[0] + ", " + qv[1] + "), pk_bf16(" + qv[2] + ", " +
+                        qv[3] + "), pk_bf16(" + qv[4] + ", " + qv[5] + "), pk_bf16(" + qv[6] + ", " + qv[7] + ")};");
+                c2.line("if (tid % 8 == 0) *(sanic_f32x2*)(&sz_lds[" + buf + "][" + row + " * 2]) = (sanic_f32x2){" + A_ + ", " +
+                        (B_.empty() ? std::string("0.0f") : (nb ? "-" : "") + B_) + "};");
+                c2.line("}");
+                continue;
+            }
             c2.line("*(sanic_u32x4*)(&b_lds[" + buf + "][" + boff + "]) = rb" + rs + sfx + ";");
             if (splitB) c2.line("*(sanic_u32x4*)(&b_lo[" + buf + "][" + boff + "]) = rl" + rs + sfx + ";");
-            if (grouped)
-                c2.line("if (tid % 8 == 0) *(sanic_f32x2*)(&sz_lds[" + buf + "][" + row + " * 2]) = (sanic_f32x2){gs" + rs + sfx + ", gz" + rs + sfx + "};");
         }
         if (BTH < NTH) c2.line("}");
         c2.indent--;
@@ -681,7 +700,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             Code tmp;
             tmp.indent = k.indent + 1;
             emit_loads(tmp, "(idx_t)0", sfx);
-            static const std::regex re(R"(const (sanic_u32x4|float) (\w+) = )");
+            static const std::regex re(R"(const (sanic_u32x4|float|unsigned short|unsigned) (\w+) = )");
             std::string t = tmp.str();
             std::set<std::string> seen;
             for (auto it = std::sregex_iterator(t.begin(), t.end(), re); it != std::sregex_iterator(); ++it) {
@@ -689,7 +708,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
                 if (name.size() > sfx.size() && name.compare(name.size() - sfx.size(), sfx.size(), sfx) == 0 &&
                     (name.rfind("pah", 0) == 0 || name.rfind("pal", 0) == 0 || name.rfind("rb", 0) == 0 ||
                      name.rfind("rl", 0) == 0 || name.rfind("ra", 0) == 0 || name.rfind("gs", 0) == 0 ||
-                     name.rfind("gz", 0) == 0) && name.rfind("rbh", 0) != 0 &&
+                     name.rfind("gz", 0) == 0 || (grouped && (name[0] == 'u' || name[0] == 'h'))) && name.rfind("rbh", 0) != 0 &&
                     name.rfind("rbl", 0) != 0 && !seen.count(name)) {
                     seen.insert(name);
                     decl.line(std::string((*it)[1]) + " " + name + ";");
@@ -704,7 +723,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             emit_loads(tmp, kt0, sfx);
             std::string t = tmp.str();
             for (auto& n : names) {
-                for (const char* ty : {"const sanic_u32x4 ", "const float "}) {
+                for (const char* ty : {"const sanic_u32x4 ", "const float ", "const unsigned short ", "const unsigned "}) {
                     const std::string from = std::string(ty) + n + " = ";
                     size_t pos = t.find(from);
                     if (pos != std::string::npos) t.replace(pos, from.size(), n + " = ");

@@ -219,6 +219,9 @@ struct VecW {
     std::string last_raw;     // the 128-bit bf16 register of the last contiguous access
     bool stream = true;           // weights are read once: non-temporal loads
     bool byte_split = false;      // packed 4-bit runs through byte-to-float converts
+    // run-invariant bf16 values loaded as raw 16-bit words in `lc`, widened in `dc` (so a caller
+    // can hold the loaded words across a loop's back edge without waiting for the load there)
+    bool raw_loads = false;
     // gcd of the k divisors of every access that does not move within a run (0: none moves
     // with k at all): such an access is constant over every aligned block of that many k
     int64_t uniform_div = 0;
@@ -338,7 +341,13 @@ struct VecW {
             for (auto& t : acc.addr.terms)
                 if (t.var == kv) uniform_div = std::gcd(uniform_div, t.div);
             std::string v = fresh("w");
-            lc.line("const float " + v + " = " + one(base) + ";");
+            if (raw_loads && acc.dtype == SANIC_BF16) {
+                const std::string h = fresh("h");
+                lc.line("const unsigned short " + h + " = " + p + "[" + base + "];");
+                dc.line("const float " + v + " = sanic_bf16(" + h + ");");
+            } else {
+                lc.line("const float " + v + " = " + one(base) + ";");
+            }
             return std::vector<std::string>(8, v);
         }
         if (jstride == 1 && acc.dtype == SANIC_BF16) {
@@ -478,9 +487,10 @@ bool render_weight_affine(const sanic_program_desc* d, int node, const std::vect
                           const std::vector<int64_t>& ext, Code& lc, Code& dc, const std::string& nn,
                           const std::string& k0, const std::string& sfx, std::vector<int>& bufs,
                           std::vector<int>& dtypes, std::vector<std::string>& q, std::string& A, std::string& B,
-                          bool& negB, int64_t& uniform_div, bool stream) {
+                          bool& negB, int64_t& uniform_div, bool stream, bool raw_loads) {
     VecW vw{d};
     vw.stream = stream;
+    vw.raw_loads = raw_loads;
     vw.nn = nn;
     vw.k0 = k0;
     vw.ptr = "wb";
