@@ -462,6 +462,11 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     }
     k.line("const idx_t wlo = wlo_a < wlo_b ? wlo_a : wlo_b, whi = whi_a > whi_b ? whi_a : whi_b;");
     k.line("const idx_t flo = wlo_a > wlo_b ? wlo_a : wlo_b, fhi = whi_a < whi_b ? whi_a : whi_b;");
+    // the bounds are wave-uniform (they depend on the block and wave only): held in scalar
+    // registers, the key loop's control and the tile classification run on the scalar unit
+    k.line("const int klo_s = __builtin_amdgcn_readfirstlane((int)klo), khi_s = __builtin_amdgcn_readfirstlane((int)khi);");
+    k.line("const int wlo_s = __builtin_amdgcn_readfirstlane((int)wlo), whi_s = __builtin_amdgcn_readfirstlane((int)whi);");
+    k.line("const int flo_s = __builtin_amdgcn_readfirstlane((int)flo), fhi_s = __builtin_amdgcn_readfirstlane((int)fhi);");
     // Edge tiles, per element: inside a row's honest window the score is the unmasked form
     // (the full-tile identity); outside it −1e30 instead of the rendered mask (a finite mask
     // gives that same value for any score below ~1e22; a −∞ mask differs only while a row has
@@ -586,27 +591,27 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
            "), (__attribute__((address_space(3))) void*)(&kv_lds[b][1][(wv + 4 * u) * 512]), 16, 0, 0);");
     k.line("  }");
     k.line("};");
-    k.line("if (klo < khi) {");
+    k.line("if (klo_s < khi_s) {");
     k.indent++;
-    k.line("fetch(klo, 0);");
-    k.line("if (klo + 64 < khi) fetch(klo + 64, 1);");
+    k.line("fetch(klo_s, 0);");
+    k.line("if (klo_s + 64 < khi_s) fetch(klo_s + 64, 1);");
     if (P.qexpr) emit_qexpr();
     k.line("int buf = 0;");
-    k.line("for (idx_t t0 = klo; t0 < khi; t0 += 64) {");
+    k.line("for (int t0 = klo_s; t0 < khi_s; t0 += 64) {");
     k.indent++;
     // this tile's transfers have landed for every wave (only the next tile's four may still be
     // in flight; loads complete in issue order). The buffer the transfer below refills was read
     // in the previous iteration: this barrier orders every wave's reads of it before the refill,
     // so the refill must stay after the barrier. The asm carries the memory clobber that keeps
     // the compiler from moving LDS accesses across the barrier.
-    k.line("if (t0 + 64 < khi) asm volatile(\"s_waitcnt vmcnt(4)\\n\\ts_barrier\" ::: \"memory\");");
+    k.line("if (t0 + 64 < khi_s) asm volatile(\"s_waitcnt vmcnt(4)\\n\\ts_barrier\" ::: \"memory\");");
     k.line("else asm volatile(\"s_waitcnt vmcnt(0)\\n\\ts_barrier\" ::: \"memory\");");
-    k.line("if (t0 + 128 < khi) fetch(t0 + 128, buf == 0 ? 2 : buf - 1);");
+    k.line("if (t0 + 128 < khi_s) fetch(t0 + 128, buf == 0 ? 2 : buf - 1);");
     // wave-uniform tile classification (scalar branches)
-    k.line("const int live = __builtin_amdgcn_readfirstlane((int)(t0 < whi && t0 + 64 > wlo));");   // some row sees it
+    k.line("const int live = t0 < whi_s && t0 + 64 > wlo_s;");   // some row sees it
     k.line("if (live) {");
     k.indent++;
-    k.line("const int full = __builtin_amdgcn_readfirstlane((int)(t0 >= flo && t0 + 64 <= fhi));");  // every row sees all
+    k.line("const int full = t0 >= flo_s && t0 + 64 <= fhi_s;");  // every row sees all
     // S^T tiles: kt (16 keys) × qt (16 queries), contraction over d in 2 steps of 32
     // both query tiles' scores first: each K fragment is read from LDS once for the two tiles
     // (measured: 2% over re-reading it per tile, the kernel being bound by LDS and MFMA issue).
@@ -642,7 +647,6 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.indent++;
     if (!s_both) scores(false);
     k.line("const int qi = (int)(q0 + qt * 16 + l16);");
-    k.line("const int kb = (int)t0 + lq * 4;");
     k.line("float sv[16];");
     k.line("float p[16];");
     k.line("float mn, alpha;");
@@ -696,6 +700,10 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     }
     // partial tiles (and scores of any other shape): the rendered leaf per element
     // (full and edge_fast are wave-uniform: one branch per tile, not a select per element)
+    // (the key indices are formed here, in the branch that uses them: the compiler would
+    // otherwise hoist them ahead of the full-tile branch)
+    k.line("int kb = t0 + lq * 4;");
+    k.line("asm volatile(\"\" : \"+v\"(kb));");
     k.line("int elo = -1, ehi = 0x7fffffff;");
     if (edge_on) {
         k.line("if (!full) {");
