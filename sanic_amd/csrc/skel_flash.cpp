@@ -424,7 +424,9 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // 16 rows of one fragment read into 2-way bank conflicts on gfx950, and the direct loads
     // write each wave's 1 KB contiguously, so the swizzle is applied to the source addresses.
     k.line("__shared__ __attribute__((aligned(16))) unsigned short kv_lds[3][2][64 * 64];");
-    k.line("const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;");
+    // (the wave index through a scalar register: the LDS destinations of the direct loads and
+    // the wave's row range are then scalar arithmetic)
+    k.line("const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);");
     k.line("const int l16 = lane & 15, lq = lane >> 4;");
     // XCD-aware block order: blockIdx mod 8 picks the KV head group, heaviest query blocks first
     const int64_t NKV = NH / P.rep;
