@@ -777,21 +777,58 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[0][ks], lsum[0], 0, 0, 0);");
     k.line("  lsum[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[1][ks], lsum[1], 0, 0, 0);");
     k.line("}");
-    k.line("#pragma unroll");
-    k.line("for (int dt = 0; dt < 4; ++dt)");
-    k.line("  #pragma unroll");
-    k.line("  for (int ks = 0; ks < 2; ++ks) {");
     if (v_rows) {
         // V rows in LDS, read transposed (ds_read_b64_tr_b16): in each 16-lane group, source
         // lane s reads 4 values of e at key row (base + s/4), e = dt·16 + 4·(s%4); lane i then
         // holds keys base + 0..3 of e = dt·16 + i — slots 0..3, and base + 16 gives slots 4..7
-        // (row + 16 has the same swizzle as row)
-        k.line("    const int vrow = ks * 32 + lq * 4 + (l16 >> 2), vcol = dt * 16 + (l16 & 3) * 4;");
-        k.line("    const unsigned short* vr = &kv_lds[buf][1][vrow * 64 + (((vcol >> 3) ^ (vrow & 7)) << 3) + (vcol & 7)];");
-        k.line("    const sanic_s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(vr));");
-        k.line("    const sanic_s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sanic_s16x4*)(vr + 16 * 64));");
-        k.line("    const bf16x8 va = __builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));");
-    } else {
+        // (row + 16 has the same swizzle as row). The reads are issued from inline asm, two
+        // value tiles (8 reads) at a time, each group completed by an explicit lgkmcnt wait
+        // that the fragments pass through: the compiler's own form of this read waits for
+        // every outstanding direct-to-LDS transfer first (vmcnt(0), i.e. the next tile's
+        // prefetch), which the loop-top barrier already orders for this buffer.
+        k.line("sanic_s16x4 vt[4][2][2];");
+        auto vreads = [&](int dt0) {
+            for (int dt = dt0; dt < dt0 + 2; dt++)
+                for (int ks = 0; ks < 2; ks++) {
+                    const std::string ix = "[" + std::to_string(dt) + "][" + std::to_string(ks) + "]";
+                    k.line("{");
+                    k.line("  const int vrow = " + std::to_string(ks * 32) + " + lq * 4 + (l16 >> 2), vcol = " + std::to_string(dt * 16) + " + (l16 & 3) * 4;");
+                    k.line("  const unsigned va_ = (unsigned)(size_t)((__attribute__((address_space(3))) const unsigned short*)&kv_lds[buf][1][vrow * 64 + (((vcol >> 3) ^ (vrow & 7)) << 3) + (vcol & 7)]);");
+                    k.line("  asm volatile(\"ds_read_b64_tr_b16 %0, %1\" : \"=v\"(vt" + ix + "[0]) : \"v\"(va_));");
+                    k.line("  asm volatile(\"ds_read_b64_tr_b16 %0, %1 offset:2048\" : \"=v\"(vt" + ix + "[1]) : \"v\"(va_));");
+                    k.line("}");
+                }
+        };
+        auto vwait = [&](int dt0) {
+            std::string ops;
+            for (int dt = dt0; dt < dt0 + 2; dt++)
+                for (int ks = 0; ks < 2; ks++)
+                    for (int h = 0; h < 2; h++)
+                        ops += std::string(ops.empty() ? "" : ", ") + "\"+v\"(vt[" + std::to_string(dt) + "][" + std::to_string(ks) + "][" + std::to_string(h) + "])";
+            k.line("asm volatile(\"s_waitcnt lgkmcnt(0)\" : " + ops + ");");
+        };
+        auto vmfma = [&](int dt0) {
+            for (int dt = dt0; dt < dt0 + 2; dt++)
+                for (int ks = 0; ks < 2; ks++) {
+                    const std::string ix = "[" + std::to_string(dt) + "][" + std::to_string(ks) + "]";
+                    const std::string va = "__builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(vt" + ix + "[0], vt" + ix + "[1], 0, 1, 2, 3, 4, 5, 6, 7))";
+                    k.line("o[" + std::to_string(dt) + "][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", pf[0][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][0], 0, 0, 0);");
+                    k.line("o[" + std::to_string(dt) + "][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", pf[1][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][1], 0, 0, 0);");
+                }
+        };
+        vreads(0);
+        vwait(0);
+        vreads(2);
+        vmfma(0);
+        vwait(2);
+        vmfma(2);
+    }
+    if (!v_rows) {
+    k.line("#pragma unroll");
+    k.line("for (int dt = 0; dt < 4; ++dt)");
+    k.line("  #pragma unroll");
+    k.line("  for (int ks = 0; ks < 2; ++ks) {");
+    {
         k.line("    const int vrow = dt * 16 + l16, vcol = ks * 32 + lq * 4;");
         k.line("    const unsigned short* vr = &kv_lds[buf][1][vrow * 64 + (((vcol >> 3) ^ (vrow & 7)) << 3) + (vcol & 7)];");
         k.line("    const unsigned short* vr2 = &kv_lds[buf][1][vrow * 64 + ((((vcol + 16) >> 3) ^ (vrow & 7)) << 3) + (vcol & 7)];");
@@ -801,6 +838,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("    o[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[0][ks], o[dt][0], 0, 0, 0);");
     k.line("    o[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[1][ks], o[dt][1], 0, 0, 0);");
     k.line("  }");
+    }
     k.indent--;
     k.line("}");
     k.line("buf = buf == 2 ? 0 : buf + 1;");
