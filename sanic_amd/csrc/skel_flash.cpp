@@ -642,7 +642,42 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         k.line("  }");
         k.line("}");
     };
+    // transposed V fragment reads (inline asm, see the P·V below) and their completion
+    auto vreads = [&](int dt0) {
+        for (int dt = dt0; dt < dt0 + 2; dt++)
+            for (int ks = 0; ks < 2; ks++) {
+                const std::string ix = "[" + std::to_string(dt) + "][" + std::to_string(ks) + "]";
+                k.line("{");
+                k.line("  const int vrow = " + std::to_string(ks * 32) + " + lq * 4 + (l16 >> 2), vcol = " + std::to_string(dt * 16) + " + (l16 & 3) * 4;");
+                k.line("  const unsigned va_ = (unsigned)(size_t)((__attribute__((address_space(3))) const unsigned short*)&kv_lds[buf][1][vrow * 64 + (((vcol >> 3) ^ (vrow & 7)) << 3) + (vcol & 7)]);");
+                k.line("  asm volatile(\"ds_read_b64_tr_b16 %0, %1\" : \"=v\"(vt" + ix + "[0]) : \"v\"(va_));");
+                k.line("  asm volatile(\"ds_read_b64_tr_b16 %0, %1 offset:2048\" : \"=v\"(vt" + ix + "[1]) : \"v\"(va_));");
+                k.line("}");
+            }
+    };
+    auto vwait = [&](int dt0) {
+        std::string ops;
+        for (int dt = dt0; dt < dt0 + 2; dt++)
+            for (int ks = 0; ks < 2; ks++)
+                for (int h = 0; h < 2; h++)
+                    ops += std::string(ops.empty() ? "" : ", ") + "\"+v\"(vt[" + std::to_string(dt) + "][" + std::to_string(ks) + "][" + std::to_string(h) + "])";
+        k.line("asm volatile(\"s_waitcnt lgkmcnt(0)\" : " + ops + ");");
+    };
+    auto vmfma = [&](int dt0) {
+        for (int dt = dt0; dt < dt0 + 2; dt++)
+            for (int ks = 0; ks < 2; ks++) {
+                const std::string ix = "[" + std::to_string(dt) + "][" + std::to_string(ks) + "]";
+                const std::string va = "__builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(vt" + ix + "[0], vt" + ix + "[1], 0, 1, 2, 3, 4, 5, 6, 7))";
+                k.line("o[" + std::to_string(dt) + "][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", pf[0][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][0], 0, 0, 0);");
+                k.line("o[" + std::to_string(dt) + "][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", pf[1][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][1], 0, 0, 0);");
+            }
+    };
+    // value tiles 0 and 1 are requested as soon as this tile's scores are issued, so they land
+    // during the softmax (16 registers; tiles 2 and 3 follow after it)
+    const bool v_early = v_rows;
+    if (v_rows) k.line("sanic_s16x4 vt[4][2][2];");
     if (s_both) scores(true);
+    if (v_early) vreads(0);
     // online softmax per query column (lane-local; the max reduces across the 4 lane groups)
     k.line("#pragma unroll");
     k.line("for (int qt = 0; qt < 2; ++qt) {");
@@ -786,37 +821,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         // that the fragments pass through: the compiler's own form of this read waits for
         // every outstanding direct-to-LDS transfer first (vmcnt(0), i.e. the next tile's
         // prefetch), which the loop-top barrier already orders for this buffer.
-        k.line("sanic_s16x4 vt[4][2][2];");
-        auto vreads = [&](int dt0) {
-            for (int dt = dt0; dt < dt0 + 2; dt++)
-                for (int ks = 0; ks < 2; ks++) {
-                    const std::string ix = "[" + std::to_string(dt) + "][" + std::to_string(ks) + "]";
-                    k.line("{");
-                    k.line("  const int vrow = " + std::to_string(ks * 32) + " + lq * 4 + (l16 >> 2), vcol = " + std::to_string(dt * 16) + " + (l16 & 3) * 4;");
-                    k.line("  const unsigned va_ = (unsigned)(size_t)((__attribute__((address_space(3))) const unsigned short*)&kv_lds[buf][1][vrow * 64 + (((vcol >> 3) ^ (vrow & 7)) << 3) + (vcol & 7)]);");
-                    k.line("  asm volatile(\"ds_read_b64_tr_b16 %0, %1\" : \"=v\"(vt" + ix + "[0]) : \"v\"(va_));");
-                    k.line("  asm volatile(\"ds_read_b64_tr_b16 %0, %1 offset:2048\" : \"=v\"(vt" + ix + "[1]) : \"v\"(va_));");
-                    k.line("}");
-                }
-        };
-        auto vwait = [&](int dt0) {
-            std::string ops;
-            for (int dt = dt0; dt < dt0 + 2; dt++)
-                for (int ks = 0; ks < 2; ks++)
-                    for (int h = 0; h < 2; h++)
-                        ops += std::string(ops.empty() ? "" : ", ") + "\"+v\"(vt[" + std::to_string(dt) + "][" + std::to_string(ks) + "][" + std::to_string(h) + "])";
-            k.line("asm volatile(\"s_waitcnt lgkmcnt(0)\" : " + ops + ");");
-        };
-        auto vmfma = [&](int dt0) {
-            for (int dt = dt0; dt < dt0 + 2; dt++)
-                for (int ks = 0; ks < 2; ks++) {
-                    const std::string ix = "[" + std::to_string(dt) + "][" + std::to_string(ks) + "]";
-                    const std::string va = "__builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(vt" + ix + "[0], vt" + ix + "[1], 0, 1, 2, 3, 4, 5, 6, 7))";
-                    k.line("o[" + std::to_string(dt) + "][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", pf[0][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][0], 0, 0, 0);");
-                    k.line("o[" + std::to_string(dt) + "][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", pf[1][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][1], 0, 0, 0);");
-                }
-        };
-        vreads(0);
+        if (!v_early) vreads(0);
         vwait(0);
         vreads(2);
         vmfma(0);
