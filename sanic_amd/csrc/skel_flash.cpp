@@ -674,10 +674,9 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     };
     // value tiles 0 and 1 are requested as soon as this tile's scores are issued, so they land
     // during the softmax (16 registers; tiles 2 and 3 follow after it)
-    const bool v_early = v_rows;
     if (v_rows) k.line("sanic_s16x4 vt[4][2][2];");
     if (s_both) scores(true);
-    if (v_early) vreads(0);
+    if (v_rows) vreads(0);
     // online softmax per query column (lane-local; the max reduces across the 4 lane groups)
     k.line("#pragma unroll");
     k.line("for (int qt = 0; qt < 2; ++qt) {");
@@ -821,7 +820,6 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         // that the fragments pass through: the compiler's own form of this read waits for
         // every outstanding direct-to-LDS transfer first (vmcnt(0), i.e. the next tile's
         // prefetch), which the loop-top barrier already orders for this buffer.
-        if (!v_early) vreads(0);
         vwait(0);
         vreads(2);
         vmfma(0);
