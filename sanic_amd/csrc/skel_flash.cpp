@@ -663,15 +663,22 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
                     ops += std::string(ops.empty() ? "" : ", ") + "\"+v\"(vt[" + std::to_string(dt) + "][" + std::to_string(ks) + "][" + std::to_string(h) + "])";
         k.line("asm volatile(\"s_waitcnt lgkmcnt(0)\" : " + ops + ");");
     };
-    auto vmfma = [&](int dt0) {
+    // qmask: bit q set = query tile q's products; pfn: the P operand array's name
+    auto vmfma = [&](int dt0, int qmask = 3, const std::string& pfn = "pf") {
         for (int dt = dt0; dt < dt0 + 2; dt++)
             for (int ks = 0; ks < 2; ks++) {
                 const std::string ix = "[" + std::to_string(dt) + "][" + std::to_string(ks) + "]";
                 const std::string va = "__builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(vt" + ix + "[0], vt" + ix + "[1], 0, 1, 2, 3, 4, 5, 6, 7))";
-                k.line("o[" + std::to_string(dt) + "][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", pf[0][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][0], 0, 0, 0);");
-                k.line("o[" + std::to_string(dt) + "][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", pf[1][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][1], 0, 0, 0);");
+                for (int q = 0; q < 2; q++)
+                    if (qmask >> q & 1)
+                        k.line("o[" + std::to_string(dt) + "][" + std::to_string(q) + "] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", " + pfn + "[" +
+                               std::to_string(q) + "][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][" + std::to_string(q) + "], 0, 0, 0);");
             }
     };
+    // the first query tile's row sum and its products with value tiles 0 and 1 are issued when
+    // the second tile's softmax begins (they need only the first tile's P), spreading the
+    // matrix-core work through the tile
+    const bool pv0 = v_rows && s_both;
     // value tiles 0 and 1 are requested as soon as this tile's scores are issued, so they land
     // during the softmax (16 registers; tiles 2 and 3 follow after it)
     if (v_rows) k.line("sanic_s16x4 vt[4][2][2];");
@@ -682,6 +689,16 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.line("for (int qt = 0; qt < 2; ++qt) {");
     k.indent++;
     if (!s_both) scores(false);
+    if (pv0) {
+        k.line("if (qt == 1) {");
+        k.line("  bf16x8 pe[1][2];");
+        k.line("  pe[0][0] = __builtin_bit_cast(bf16x8, pw[0][0]); pe[0][1] = __builtin_bit_cast(bf16x8, pw[0][1]);");
+        k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pe[0][0], lsum[0], 0, 0, 0);");
+        k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pe[0][1], lsum[0], 0, 0, 0);");
+        vwait(0);
+        vmfma(0, 1, "pe");
+        k.line("}");
+    }
     k.line("const int qi = (int)(q0 + qt * 16 + l16);");
     k.line("float sv[16];");
     k.line("float p[16];");
@@ -808,7 +825,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // O^T += V^T · P^T ; V^T A operand: row e = dt·16 + l16, keys in the same slot order
     k.line("#pragma unroll");
     k.line("for (int ks = 0; ks < 2; ++ks) {");
-    k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[0][ks], lsum[0], 0, 0, 0);");
+    if (!pv0) k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[0][ks], lsum[0], 0, 0, 0);");
     k.line("  lsum[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[1][ks], lsum[1], 0, 0, 0);");
     k.line("}");
     if (v_rows) {
@@ -820,9 +837,9 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         // that the fragments pass through: the compiler's own form of this read waits for
         // every outstanding direct-to-LDS transfer first (vmcnt(0), i.e. the next tile's
         // prefetch), which the loop-top barrier already orders for this buffer.
-        vwait(0);
+        if (!pv0) vwait(0);
         vreads(2);
-        vmfma(0);
+        vmfma(0, pv0 ? 2 : 3);
         vwait(2);
         vmfma(2);
     }
