@@ -615,11 +615,12 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.indent++;
     k.line("const int full = t0 >= flo_s && t0 + 64 <= fhi_s;");  // every row sees all
     // S^T tiles: kt (16 keys) × qt (16 queries), contraction over d in 2 steps of 32
-    // both query tiles' scores first: each K fragment is read from LDS once for the two tiles
-    // (measured: 2% over re-reading it per tile, the kernel being bound by LDS and MFMA issue).
-    // The split variant and the rendered-mask reference variant keep one query tile's scores
-    // live at a time (with both live they spill 12–13 registers); the products are the same
-    // MFMAs in the same order either way.
+    // s_both: both query tiles' scores stay live through the tile. With V^T in memory both are
+    // computed first, each K fragment read from LDS once for the two tiles; with V rows the
+    // second tile's scores are issued later (below) and read the K fragments again. The split
+    // variant and the rendered-mask reference variant keep one query tile's scores live at a
+    // time (with both live they spill 12–13 registers); the products are the same MFMAs in the
+    // same order either way.
     const bool s_both = SPL == 1 && fvar != 3;
     k.line("f32x4 s[4][2];");
     k.line("sanic_u32x4 pw[2][2];");
@@ -682,7 +683,16 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // value tiles 0 and 1 are requested as soon as this tile's scores are issued, so they land
     // during the softmax (16 registers; tiles 2 and 3 follow after it)
     if (v_rows) k.line("sanic_s16x4 vt[4][2][2];");
-    if (s_both) scores(true);
+    // the second query tile's scores (its K fragments read again) are issued with the first
+    // tile's P·V products below, after the first tile's softmax, so the matrix cores get work
+    // in three spread-out bursts per tile rather than two
+    const bool s1late = s_both && v_rows;
+    if (s1late) {
+        k.line("{");
+        k.line("const int qt = 0;");
+        scores(false);
+        k.line("}");
+    } else if (s_both) scores(true);
     if (v_rows) vreads(0);
     // online softmax per query column (lane-local; the max reduces across the 4 lane groups)
     k.line("#pragma unroll");
@@ -691,6 +701,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     if (!s_both) scores(false);
     if (pv0) {
         k.line("if (qt == 1) {");
+        if (s1late) scores(false);
         k.line("  bf16x8 pe[1][2];");
         k.line("  pe[0][0] = __builtin_bit_cast(bf16x8, pw[0][0]); pe[0][1] = __builtin_bit_cast(bf16x8, pw[0][1]);");
         k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pe[0][0], lsum[0], 0, 0, 0);");
