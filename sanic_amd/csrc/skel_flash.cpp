@@ -676,12 +676,12 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
                                std::to_string(q) + "][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][" + std::to_string(q) + "], 0, 0, 0);");
             }
     };
-    // the first query tile's row sum and its products with value tiles 0 and 1 are issued when
-    // the second tile's softmax begins (they need only the first tile's P), spreading the
-    // matrix-core work through the tile
+    // the first query tile's row sum and all its P·V products are issued when the second
+    // tile's softmax begins (they need only the first tile's P; value tiles 2 and 3 are read
+    // there), spreading the matrix-core work through the tile
     const bool pv0 = v_rows && s_both;
-    // value tiles 0 and 1 are requested as soon as this tile's scores are issued, so they land
-    // during the softmax (16 registers; tiles 2 and 3 follow after it)
+    // value tiles 0 and 1 are requested as soon as this tile's first scores are issued, so they
+    // land during the softmax (16 registers; tiles 2 and 3 follow with the first P·V products)
     if (v_rows) k.line("sanic_s16x4 vt[4][2][2];");
     // the second query tile's scores (its K fragments read again) are issued with the first
     // tile's P·V products below, after the first tile's softmax, so the matrix cores get work
@@ -708,6 +708,9 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pe[0][1], lsum[0], 0, 0, 0);");
         vwait(0);
         vmfma(0, 1, "pe");
+        vreads(2);
+        vwait(2);
+        vmfma(2, 1, "pe");
         k.line("}");
     }
     k.line("const int qi = (int)(q0 + qt * 16 + l16);");
@@ -848,11 +851,13 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         // that the fragments pass through: the compiler's own form of this read waits for
         // every outstanding direct-to-LDS transfer first (vmcnt(0), i.e. the next tile's
         // prefetch), which the loop-top barrier already orders for this buffer.
-        if (!pv0) vwait(0);
-        vreads(2);
+        if (!pv0) {
+            vwait(0);
+            vreads(2);
+        }
         vmfma(0, pv0 ? 2 : 3);
-        vwait(2);
-        vmfma(2);
+        if (!pv0) vwait(2);
+        vmfma(2, pv0 ? 2 : 3);
     }
     if (!v_rows) {
     k.line("#pragma unroll");
