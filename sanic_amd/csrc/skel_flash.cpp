@@ -615,12 +615,11 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     k.indent++;
     k.line("const int full = t0 >= flo_s && t0 + 64 <= fhi_s;");  // every row sees all
     // S^T tiles: kt (16 keys) × qt (16 queries), contraction over d in 2 steps of 32
-    // s_both: both query tiles' scores stay live through the tile. With V^T in memory both are
-    // computed first, each K fragment read from LDS once for the two tiles; with V rows the
-    // second tile's scores are issued later (below) and read the K fragments again. The split
-    // variant and the rendered-mask reference variant keep one query tile's scores live at a
-    // time (with both live they spill 12–13 registers); the products are the same MFMAs in the
-    // same order either way.
+    // both query tiles' scores first: each K fragment is read from LDS once for the two tiles
+    // (measured: 2% over re-reading it per tile, the kernel being bound by LDS and MFMA issue).
+    // The split variant and the rendered-mask reference variant keep one query tile's scores
+    // live at a time (with both live they spill 12–13 registers); the products are the same
+    // MFMAs in the same order either way.
     const bool s_both = SPL == 1 && fvar != 3;
     k.line("f32x4 s[4][2];");
     k.line("sanic_u32x4 pw[2][2];");
@@ -643,76 +642,12 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         k.line("  }");
         k.line("}");
     };
-    // transposed V fragment reads (inline asm, see the P·V below) and their completion
-    auto vreads = [&](int dt0) {
-        for (int dt = dt0; dt < dt0 + 2; dt++)
-            for (int ks = 0; ks < 2; ks++) {
-                const std::string ix = "[" + std::to_string(dt) + "][" + std::to_string(ks) + "]";
-                k.line("{");
-                k.line("  const int vrow = " + std::to_string(ks * 32) + " + lq * 4 + (l16 >> 2), vcol = " + std::to_string(dt * 16) + " + (l16 & 3) * 4;");
-                k.line("  const unsigned va_ = (unsigned)(size_t)((__attribute__((address_space(3))) const unsigned short*)&kv_lds[buf][1][vrow * 64 + (((vcol >> 3) ^ (vrow & 7)) << 3) + (vcol & 7)]);");
-                k.line("  asm volatile(\"ds_read_b64_tr_b16 %0, %1\" : \"=v\"(vt" + ix + "[0]) : \"v\"(va_));");
-                k.line("  asm volatile(\"ds_read_b64_tr_b16 %0, %1 offset:2048\" : \"=v\"(vt" + ix + "[1]) : \"v\"(va_));");
-                k.line("}");
-            }
-    };
-    auto vwait = [&](int dt0) {
-        std::string ops;
-        for (int dt = dt0; dt < dt0 + 2; dt++)
-            for (int ks = 0; ks < 2; ks++)
-                for (int h = 0; h < 2; h++)
-                    ops += std::string(ops.empty() ? "" : ", ") + "\"+v\"(vt[" + std::to_string(dt) + "][" + std::to_string(ks) + "][" + std::to_string(h) + "])";
-        k.line("asm volatile(\"s_waitcnt lgkmcnt(0)\" : " + ops + ");");
-    };
-    // qmask: bit q set = query tile q's products; pfn: the P operand array's name
-    auto vmfma = [&](int dt0, int qmask = 3, const std::string& pfn = "pf") {
-        for (int dt = dt0; dt < dt0 + 2; dt++)
-            for (int ks = 0; ks < 2; ks++) {
-                const std::string ix = "[" + std::to_string(dt) + "][" + std::to_string(ks) + "]";
-                const std::string va = "__builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(vt" + ix + "[0], vt" + ix + "[1], 0, 1, 2, 3, 4, 5, 6, 7))";
-                for (int q = 0; q < 2; q++)
-                    if (qmask >> q & 1)
-                        k.line("o[" + std::to_string(dt) + "][" + std::to_string(q) + "] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", " + pfn + "[" +
-                               std::to_string(q) + "][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][" + std::to_string(q) + "], 0, 0, 0);");
-            }
-    };
-    // the first query tile's row sum and all its P·V products are issued when the second
-    // tile's softmax begins (they need only the first tile's P; value tiles 2 and 3 are read
-    // there), spreading the matrix-core work through the tile
-    const bool pv0 = v_rows && s_both;
-    // value tiles 0 and 1 are requested as soon as this tile's first scores are issued, so they
-    // land during the softmax (16 registers; tiles 2 and 3 follow with the first P·V products)
-    if (v_rows) k.line("sanic_s16x4 vt[4][2][2];");
-    // the second query tile's scores (its K fragments read again) are issued with the first
-    // tile's P·V products below, after the first tile's softmax, so the matrix cores get work
-    // in three spread-out bursts per tile rather than two
-    const bool s1late = s_both && v_rows;
-    if (s1late) {
-        k.line("{");
-        k.line("const int qt = 0;");
-        scores(false);
-        k.line("}");
-    } else if (s_both) scores(true);
-    if (v_rows) vreads(0);
+    if (s_both) scores(true);
     // online softmax per query column (lane-local; the max reduces across the 4 lane groups)
     k.line("#pragma unroll");
     k.line("for (int qt = 0; qt < 2; ++qt) {");
     k.indent++;
     if (!s_both) scores(false);
-    if (pv0) {
-        k.line("if (qt == 1) {");
-        if (s1late) scores(false);
-        k.line("  bf16x8 pe[1][2];");
-        k.line("  pe[0][0] = __builtin_bit_cast(bf16x8, pw[0][0]); pe[0][1] = __builtin_bit_cast(bf16x8, pw[0][1]);");
-        k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pe[0][0], lsum[0], 0, 0, 0);");
-        k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pe[0][1], lsum[0], 0, 0, 0);");
-        vwait(0);
-        vmfma(0, 1, "pe");
-        vreads(2);
-        vwait(2);
-        vmfma(2, 1, "pe");
-        k.line("}");
-    }
     k.line("const int qi = (int)(q0 + qt * 16 + l16);");
     k.line("float sv[16];");
     k.line("float p[16];");
@@ -839,7 +774,7 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
     // O^T += V^T · P^T ; V^T A operand: row e = dt·16 + l16, keys in the same slot order
     k.line("#pragma unroll");
     k.line("for (int ks = 0; ks < 2; ++ks) {");
-    if (!pv0) k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[0][ks], lsum[0], 0, 0, 0);");
+    k.line("  lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[0][ks], lsum[0], 0, 0, 0);");
     k.line("  lsum[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[1][ks], lsum[1], 0, 0, 0);");
     k.line("}");
     if (v_rows) {
@@ -851,13 +786,42 @@ bool lower_flash_prefill(const sanic_program_desc* d, int si, int64_t& scratch, 
         // that the fragments pass through: the compiler's own form of this read waits for
         // every outstanding direct-to-LDS transfer first (vmcnt(0), i.e. the next tile's
         // prefetch), which the loop-top barrier already orders for this buffer.
-        if (!pv0) {
-            vwait(0);
-            vreads(2);
-        }
-        vmfma(0, pv0 ? 2 : 3);
-        if (!pv0) vwait(2);
-        vmfma(2, pv0 ? 2 : 3);
+        k.line("sanic_s16x4 vt[4][2][2];");
+        auto vreads = [&](int dt0) {
+            for (int dt = dt0; dt < dt0 + 2; dt++)
+                for (int ks = 0; ks < 2; ks++) {
+                    const std::string ix = "[" + std::to_string(dt) + "][" + std::to_string(ks) + "]";
+                    k.line("{");
+                    k.line("  const int vrow = " + std::to_string(ks * 32) + " + lq * 4 + (l16 >> 2), vcol = " + std::to_string(dt * 16) + " + (l16 & 3) * 4;");
+                    k.line("  const unsigned va_ = (unsigned)(size_t)((__attribute__((address_space(3))) const unsigned short*)&kv_lds[buf][1][vrow * 64 + (((vcol >> 3) ^ (vrow & 7)) << 3) + (vcol & 7)]);");
+                    k.line("  asm volatile(\"ds_read_b64_tr_b16 %0, %1\" : \"=v\"(vt" + ix + "[0]) : \"v\"(va_));");
+                    k.line("  asm volatile(\"ds_read_b64_tr_b16 %0, %1 offset:2048\" : \"=v\"(vt" + ix + "[1]) : \"v\"(va_));");
+                    k.line("}");
+                }
+        };
+        auto vwait = [&](int dt0) {
+            std::string ops;
+            for (int dt = dt0; dt < dt0 + 2; dt++)
+                for (int ks = 0; ks < 2; ks++)
+                    for (int h = 0; h < 2; h++)
+                        ops += std::string(ops.empty() ? "" : ", ") + "\"+v\"(vt[" + std::to_string(dt) + "][" + std::to_string(ks) + "][" + std::to_string(h) + "])";
+            k.line("asm volatile(\"s_waitcnt lgkmcnt(0)\" : " + ops + ");");
+        };
+        auto vmfma = [&](int dt0) {
+            for (int dt = dt0; dt < dt0 + 2; dt++)
+                for (int ks = 0; ks < 2; ks++) {
+                    const std::string ix = "[" + std::to_string(dt) + "][" + std::to_string(ks) + "]";
+                    const std::string va = "__builtin_bit_cast(bf16x8, (sanic_s16x8)__builtin_shufflevector(vt" + ix + "[0], vt" + ix + "[1], 0, 1, 2, 3, 4, 5, 6, 7))";
+                    k.line("o[" + std::to_string(dt) + "][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", pf[0][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][0], 0, 0, 0);");
+                    k.line("o[" + std::to_string(dt) + "][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(" + va + ", pf[1][" + std::to_string(ks) + "], o[" + std::to_string(dt) + "][1], 0, 0, 0);");
+                }
+        };
+        vreads(0);
+        vwait(0);
+        vreads(2);
+        vmfma(0);
+        vwait(2);
+        vmfma(2);
     }
     if (!v_rows) {
     k.line("#pragma unroll");
