@@ -67,8 +67,15 @@ void emit_window(Renderer& R, Code& code, const sanic_stage& st, const std::vect
 int64_t dtype_bytes(int dt, int64_t n);
 // Last-arriver handshake: the workgroups sharing counter `cnt` each add 1 once their partials
 // are stored; `flag` (a __shared__ int it declares) is true in the one that arrives last.
+// With xcd_local every workgroup sharing `cnt` runs on one XCD and exchanges data through
+// sanic_stx / sanic_ldx (that XCD's L2); otherwise through sanic_st / sanic_ld (device-coherent).
 void emit_arrival(Code& k, const std::string& flag, const std::string& tid, const std::string& cnt,
-                  const std::string& expected);
+                  const std::string& expected, bool xcd_local = false);
+// Workgroups are dispatched round-robin over the 8 XCDs by linear block index; the runtime
+// checks that once per process (set_xcd_local) and kernels whose merging workgroups share
+// blockIdx mod 8 then exchange partials through the L2 of their XCD.
+void set_xcd_local(bool on);
+bool xcd_local_enabled();
 void validate(const sanic_program_desc* d);
 
 // The MI355X figures the cost model reads (the same numbers sanic_hip_specs reports).

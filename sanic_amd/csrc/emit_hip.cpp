@@ -43,11 +43,24 @@ static std::vector<int64_t> shp(const sanic_node& n) { return {n.shape, n.shape 
 // workgroup's barrier and so before every one of its threads reads the partials. The
 // waitcnt makes each wave's own stores complete before the barrier, so the release has nothing
 // of theirs left in flight.
+static bool g_xcd_local = true;
+void set_xcd_local(bool on) { g_xcd_local = on; }
+bool xcd_local_enabled() { return g_xcd_local && !getenv("SANIC_HIP_AGENT_MERGE"); }
+
 void emit_arrival(Code& k, const std::string& flag, const std::string& tid, const std::string& cnt,
-                  const std::string& expected) {
+                  const std::string& expected, bool xcd_local) {
     k.line("__shared__ int " + flag + ";");
     k.line("__builtin_amdgcn_s_waitcnt(0);");
     k.line("__syncthreads();");
+    if (xcd_local) {
+        // one XCD: the waitcnt above has every wave's partial stores acknowledged by the XCD's
+        // L2 before the barrier, the counter RMW is performed there after them, and the last
+        // arriver's loads issue after its RMW returns (the barrier below) — no L2 write-back,
+        // no invalidation, no round trip past the L2
+        k.line("if (" + tid + " == 0) " + flag + " = __hip_atomic_fetch_add(" + cnt + ", 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (" + expected + ") - 1u;");
+        k.line("__syncthreads();");
+        return;
+    }
     // release on every arrival; only the last arriver, which goes on to read the others'
     // partials, takes the acquire (a fence after its RMW, which reads the release sequence of
     // every earlier arrival) — the others skip the acquire's cache invalidation
@@ -345,6 +358,15 @@ template <class T> __device__ __forceinline__ T sanic_ld(const T* p) {
 }
 template <class T> __device__ __forceinline__ void sanic_st(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// data exchanged between workgroups of one XCD (the kernel places every workgroup that shares an
+// arrival counter on one XCD): plain accesses through that XCD's L2 — stores write through the
+// L1, and the merging workgroup reads each partial once per launch, so its L1 (invalidated at
+// kernel start) holds no earlier copy
+template <class T> __device__ __forceinline__ T sanic_ldx(const T* p) { return *p; }
+template <class T> __device__ __forceinline__ void sanic_stx(T* p, T v) { *p = v; }
+__device__ __forceinline__ sanic_f32x4 sanic_ldx4(const float* base, unsigned off_bytes) {
+  return *(const sanic_f32x4*)((const char*)base + off_bytes);
 }
 // Cross-lane reductions without the LDS pipe (__shfl_xor lowers to ds_bpermute, ~100 cycles a
 // step on a dependent chain): DPP within rows of 16 lanes — quad_perm [1,0,3,2] (lane ^ 1),

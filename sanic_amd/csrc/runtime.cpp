@@ -43,6 +43,37 @@ struct sanic_hip_device {
 static const size_t kStaticScratchBytes = size_t(32) << 20;
 static __device__ __align__(256) char scratch[kStaticScratchBytes];
 
+// Which XCD each workgroup of a launch runs on (the hardware register XCC_ID): kernels that let
+// the workgroups sharing an arrival counter exchange partials through one XCD's L2 rely on the
+// dispatcher's round-robin placement (linear block b on XCD b mod 8). Checked once per GPU at
+// its first open, on a grid of an odd size; any other placement switches those kernels to the
+// device-coherent exchange for the rest of the process.
+__global__ void sanic_xcc_probe(int* out) {
+    if (threadIdx.x == 0) {
+        unsigned v;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+        out[blockIdx.x] = (int)(v & 0xF);
+    }
+}
+
+static bool probe_xcd_round_robin(hipStream_t stream, char* dev_buf) {
+    const int kBlocks = 1001;
+    int* out = (int*)dev_buf;
+    hipLaunchKernelGGL(sanic_xcc_probe, dim3(kBlocks), dim3(64), 0, stream, out);
+    if (hipGetLastError() != hipSuccess) return false;
+    std::vector<int> h(kBlocks, -1);
+    if (hipMemcpyAsync(h.data(), out, kBlocks * sizeof(int), hipMemcpyDeviceToHost, stream) != hipSuccess) return false;
+    if (hipStreamSynchronize(stream) != hipSuccess) return false;
+    bool seen[16] = {};
+    for (int b = 0; b < kBlocks; b++) {
+        if (h[b] != b % 8) return false;
+        seen[h[b]] = true;
+    }
+    for (int x = 0; x < 8; x++)
+        if (!seen[x]) return false;
+    return true;
+}
+
 // One event per GPU marking the end of the last sanic_hip_execute_static call's work on that
 // GPU. Each call makes its stream wait on it before touching the scratch and records it after
 // enqueueing, so calls from different device handles (each with its own stream) on one GPU are
@@ -361,6 +392,8 @@ int sanic_hip_open(int ordinal, sanic_hip_device** out) {
                     fail(SANIC_ERR_BACKEND, std::string("hipEventCreateWithFlags: ") + hipGetErrorString(ee));
                 }
                 g_static_done[ordinal] = ev;
+                // first open of this GPU: nothing has used its static scratch yet
+                if (!probe_xcd_round_robin(d->stream, d->scratch_ptr)) set_xcd_local(false);
             }
         }
         *out = d;

@@ -1517,6 +1517,7 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
     if (N % (SW * 8) == 0 && K % (RPS * NWV * KSL) == 0 && K <= 8192) {
         const int SC = (int)P.cslots.size(), SR = (int)P.rslots.size();
         const int64_t NS = N / SW, KH = K / KSL, KQ = KH / NWV, IT = KQ / RPS;   // strips, slice rows, rows per wave, row steps
+        const bool xl = KSL > 1 && xcd_local_enabled();
         int64_t part_off = 0, counter_off = 0;
         if (KSL > 1) {
             part_off = scratch;
@@ -1616,12 +1617,13 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
             // this slice's column sums to scratch, then the later of the strip's workgroups
             // finishes: the slices' partials added in slice order
             k.line("if (t < " + std::to_string(SW) + ") {");
+            // (the slices of a strip share blockIdx mod 8, i.e. one XCD: through its L2)
             for (int cs = 0; cs < SC; cs++)
-                k.line("  sanic_st(a.scratch + " + std::to_string(part_off / 4) + " + (slice * " + std::to_string(SC) + " + " + std::to_string(cs) + ") * " +
-                       std::to_string(N) + " + strip * " + std::to_string(SW) + " + t, " + wave_sum_of(cs) + ");");
+                k.line(std::string("  ") + (xl ? "sanic_stx" : "sanic_st") + "(a.scratch + " + std::to_string(part_off / 4) + " + (slice * " + std::to_string(SC) + " + " +
+                       std::to_string(cs) + ") * " + std::to_string(N) + " + strip * " + std::to_string(SW) + " + t, " + wave_sum_of(cs) + ");");
             k.line("}");
             k.line("unsigned* cnt = (unsigned*)((char*)a.scratch + " + std::to_string(counter_off) + ") + strip;");
-            emit_arrival(k, "sanic_last", "t", "cnt", std::to_string(KSL) + "u");
+            emit_arrival(k, "sanic_last", "t", "cnt", std::to_string(KSL) + "u", xl);
             k.line("if (!sanic_last) return;");
             k.line("if (t == 0) sanic_st(cnt, 0u);");
         }
@@ -1633,7 +1635,8 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
             std::string sum;
             if (KSL > 1) {
                 for (int q = 0; q < KSL; q++) {
-                    std::string pq = "sanic_ld(a.scratch + " + std::to_string(part_off / 4) + " + (" + std::to_string(q * SC + cs) + ") * " + std::to_string(N) + " + nn)";
+                    std::string pq = std::string(xl ? "sanic_ldx" : "sanic_ld") + "(a.scratch + " + std::to_string(part_off / 4) + " + (" + std::to_string(q * SC + cs) + ") * " +
+                                     std::to_string(N) + " + nn)";
                     sum = q ? "(" + sum + " + " + pq + ")" : pq;
                 }
             } else {
@@ -1658,7 +1661,7 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         std::ostringstream src;
         src << kPrelude << R.args_struct(KSL > 1 ? std::vector<std::string>{"float* __restrict__ scratch"} : std::vector<std::string>{})
             << "extern \"C\" __global__ void __launch_bounds__(" << NT << ") " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
-        out.kernel_kind = "skeleton:gemv_kmajor[strips " + std::to_string(SW) + (KSL > 1 ? " x" + std::to_string(KSL) + " slices" : "") + "]";
+        out.kernel_kind = "skeleton:gemv_kmajor[strips " + std::to_string(SW) + (KSL > 1 ? " x" + std::to_string(KSL) + " slices" : "") + "]" + (xl ? "+xcd" : "");
         out.source = "// sched-strategy: max-memory-clause\n" + src.str();   // B1 12.26 → 12.07 µs
         out.variants = 4;
         std::vector<Arg> args = R.arg_list();

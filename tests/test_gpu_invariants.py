@@ -268,6 +268,28 @@ def test_soak_sliced_strip_gemv(dev):
     assert "x4 slices" in exe.stage_kernel(0), exe.stage_kernel(0)
 
 
+def test_xcd_local_merge_matches_device_coherent(dev, monkeypatch):
+    """The K-major GEMV's slices meet through one XCD's L2 (the runtime found round-robin XCD
+    placement at device open) or through device-coherent memory (SANIC_HIP_AGENT_MERGE): the
+    same additions in the same order, so bit-identical outputs."""
+    K, N = 2048, 8192
+    wbits = oracle.synth_bf16(953, K * N, "normal", 0.0, 0.02)
+    vals = {"x": oracle.synth(951, K, dtype=ir.BF16).reshape(1, K),
+            "g": oracle.synth(952, K, "normal", 1.0, 0.02, dtype=ir.BF16),
+            "W": from_bf16_bits(wbits).astype(np.float64).reshape(K, N)}
+    got = {}
+    for mode in ("xcd", "agent"):
+        if mode == "agent":
+            monkeypatch.setenv("SANIC_HIP_AGENT_MERGE", "1")
+        prog = configs.rmsnorm_projection(M=1, K=K, N=N, kmajor=True)
+        out, exe = run_on_gpu(dev, prog, vals)
+        kind = exe.stage_kernel(0)
+        print(mode, kind, flush=True)
+        assert kind.endswith("+xcd") == (mode == "xcd"), kind
+        got[mode] = out["y"]
+    assert np.array_equal(got["xcd"], got["agent"])
+
+
 def test_soak_flash_split_variant(dev):
     """The flash split variant (two workgroups per block exchange (m, ℓ, o) partials, the later
     one combines in a fixed operand order): 5000 replays, bit-identical."""
