@@ -12,6 +12,7 @@
 //   rowwrite  the in-place `where(at_pos, new, cache)` stage: launched over the cache row only.
 #include <numeric>
 #include <algorithm>
+#include <regex>
 #include <cmath>
 #include <set>
 
@@ -1536,7 +1537,26 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
         k.line("const idx_t slice = (blockIdx.x / 8) % " + std::to_string(KSL) + ";");
         k.line("const idx_t n0 = strip * " + std::to_string(SW) + " + (lane & " + std::to_string(LPR - 1) + ") * 8;");
         const std::string krow0 = "(slice * " + std::to_string(KH) + " + (idx_t)wv * " + std::to_string(KQ) + ")";
-        // weight loads first (every row step of this lane), then the LDS prologue
+        // the row leaves' values of this thread's K / NT rows are requested first, then the
+        // weight loads (every row step of this lane), then the LDS prologue on those values: it
+        // waits only for the earliest requests, so it runs while the weights are in flight
+        const int64_t PR = (K + NT - 1) / NT;     // prologue rows per thread (the last partial)
+        auto pro_row = [&](int64_t i) {
+            const std::string r = "(t + " + std::to_string(i * NT) + ")";
+            return (i + 1) * NT <= K ? r : "(" + r + " < " + std::to_string(K) + " ? " + r + " : 0)";
+        };
+        for (int64_t i = 0; i < PR; i++) {
+            const std::string kr = pro_row(i);
+            R.memo.emplace_back();
+            for (int l = 0; l < st.n_leaves; l++) {
+                if (l == P.w) continue;
+                const sanic_node& ln = d->nodes[st.leaf[l]];
+                std::vector<std::string> lc(ln.rank);
+                for (int j = 0; j < ln.rank; j++) lc[j] = st.bind[l][j] == SANIC_BIND_STREAM ? kr : "0";
+                k.line("const float x" + std::to_string(l) + "_p" + std::to_string(i) + " = " + R.value(k, st.leaf[l], lc) + ";");
+            }
+            R.memo.pop_back();
+        }
         std::vector<std::vector<std::string>> wv_(IT);
         Code wdc;
         wdc.indent = k.indent;
@@ -1554,26 +1574,33 @@ bool lower_gemv_kmajor(const sanic_program_desc* d, int si, int64_t& scratch, Lo
             if (i == 0)
                 for (size_t b = 0; b < vw.bufs.size(); b++)
                     k.line("const " + std::string(ctype_of(vw.dtypes[b])) + "* __restrict__ wb" + std::to_string(b) + " = " + R.param(vw.bufs[b]) + ";");
-            k.s << l1.str();
+            // one bf16 weight buffer under 4 GB: 32-bit byte offsets from its uniform base (one
+            // address register per load instead of two, so every row's request issues before
+            // the prologue's first wait)
+            std::string ls = l1.str();
+            if (vw.bufs.size() == 1 && vw.dtypes[0] == SANIC_BF16 && K * N * 2 < (int64_t(1) << 32)) {
+                ls = std::regex_replace(ls, std::regex("const idx_t (ad\\w+) = "), "const unsigned $1 = ");
+                ls = std::regex_replace(ls, std::regex(R"(\(wb0 \+ (ad\w+)\))"), "((const unsigned short*)((const char*)wb0 + $1 * 2u))");
+            }
+            k.s << ls;
         }
-        // activation factors of every k into LDS; this workgroup's row slots
+        // activation factors of every k into LDS; this workgroup's row slots (after the weight
+        // requests: the scheduler would otherwise hoist this arithmetic, and its waits, above them)
+        k.line("__builtin_amdgcn_sched_barrier(0);");
         for (int r = 0; r < SR; r++) k.line("float rpart" + std::to_string(r) + " = 0.0f;");
-        k.line("for (int kr = t; kr < " + std::to_string(K) + "; kr += " + std::to_string(NT) + ") {");
-        k.indent++;
-        R.memo.emplace_back();
-        for (int l = 0; l < st.n_leaves; l++) {
-            if (l == P.w) continue;
-            const sanic_node& ln = d->nodes[st.leaf[l]];
-            std::vector<std::string> lc(ln.rank);
-            for (int j = 0; j < ln.rank; j++) lc[j] = st.bind[l][j] == SANIC_BIND_STREAM ? "kr" : "0";
-            k.line("const float x" + std::to_string(l) + " = " + R.value(k, st.leaf[l], lc) + ";");
+        for (int64_t i = 0; i < PR; i++) {
+            const std::string kr = "(t + " + std::to_string(i * NT) + ")", ps = "_p" + std::to_string(i);
+            R.memo.emplace_back();
+            auto item = [&](int it) { return "x" + std::to_string(it) + ps; };
+            k.line((i + 1) * NT <= K ? "{" : "if (" + kr + " < " + std::to_string(K) + ") {");
+            for (int l = 0; l < st.n_leaves; l++)
+                if (l != P.w) k.line("  const float x" + std::to_string(l) + " = " + item(l) + ";");
+            for (int cs = 0; cs < SC; cs++)
+                k.line("  fl[" + std::to_string(cs) + "][" + kr + "] = " + expr_without(R, k, c.into[P.cslots[cs]], P.w, "x") + ";");
+            for (int r = 0; r < SR; r++) k.line("  rpart" + std::to_string(r) + " += " + R.expr(k, c.into[P.rslots[r]], "x", "", "", "") + ";");
+            k.line("}");
+            R.memo.pop_back();
         }
-        for (int cs = 0; cs < SC; cs++)
-            k.line("fl[" + std::to_string(cs) + "][kr] = " + expr_without(R, k, c.into[P.cslots[cs]], P.w, "x") + ";");
-        for (int r = 0; r < SR; r++) k.line("rpart" + std::to_string(r) + " += " + R.expr(k, c.into[P.rslots[r]], "x", "", "", "") + ";");
-        R.memo.pop_back();
-        k.indent--;
-        k.line("}");
         for (int r = 0; r < SR; r++) {
             std::string rs = std::to_string(r);
             k.line("rpart" + rs + " = sanic_wave_sum(rpart" + rs + ");");
