@@ -18,6 +18,7 @@
 #include "skeletons.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -43,9 +44,11 @@ static std::vector<int64_t> shp(const sanic_node& n) { return {n.shape, n.shape 
 // workgroup's barrier and so before every one of its threads reads the partials. The
 // waitcnt makes each wave's own stores complete before the barrier, so the release has nothing
 // of theirs left in flight.
-static bool g_xcd_local = true;
-void set_xcd_local(bool on) { g_xcd_local = on; }
-bool xcd_local_enabled() { return g_xcd_local && !getenv("SANIC_HIP_AGENT_MERGE"); }
+// true until a GPU's probe at its first open finds another placement (read by lowerings that
+// may run on other threads)
+static std::atomic<bool> g_xcd_local{true};
+void set_xcd_local(bool on) { g_xcd_local.store(on, std::memory_order_relaxed); }
+bool xcd_local_enabled() { return g_xcd_local.load(std::memory_order_relaxed) && !getenv("SANIC_HIP_AGENT_MERGE"); }
 
 void emit_arrival(Code& k, const std::string& flag, const std::string& tid, const std::string& cnt,
                   const std::string& expected, bool xcd_local) {
