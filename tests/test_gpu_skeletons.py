@@ -39,7 +39,7 @@ def test_b1_rmsnorm_gemv_rows_layout(dev, M):
 
 
 @pytest.mark.parametrize("variant", [0, 1, 2, 3])
-@pytest.mark.parametrize("K,N", [(2048, 8192), (256, 1024)])
+@pytest.mark.parametrize("K,N", [(2048, 8192), (256, 1024), (640, 1024)])
 def test_b1_rmsnorm_gemv_kmajor(dev, K, N, variant):
     """Config B1 as configured: W bf16 [K, N] (K-major), the N-contiguous gemv skeleton in every
     strip form (0: 128 columns × 4 K slices meeting in scratch; 1: 32-column whole-K strips;
