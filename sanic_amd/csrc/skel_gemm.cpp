@@ -265,7 +265,13 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         grouped = render_weight_affine(d, st.leaf[P.w], cw, {N, K}, l1, d1, "nn", "k0", "_g", gb, gd, qv, A_, B_, gneg, ud, false) &&
                   ud % 64 == 0 && qv.size() == 8;
     }
-    const int BNS = BN + 8;                   // [k][n] B tile row stride (bf16)
+    // [k][n] B tile row stride (bf16). The transposed operand read takes, per 32 lanes, 32
+    // bytes of each of rows r..r+3 and r+8..r+11: a stride of 72 words puts rows r..r+3 on
+    // disjoint 8-bank runs of the 64 banks, and flipping the 64-element half of the row for
+    // rows with bit 3 set moves r+8..r+11 onto the other 32 banks (B2: LDS bank-conflict
+    // cycles 2.1 M → 0 per launch, LDS-busy cycles 9.5 M → 7.4 M); other widths keep BN + 8
+    const bool bswz = BN == 128;
+    const int BNS = BN + (bswz ? 16 : 8);
     // row leaves vector forms over vars {0: m, 1: k}
     std::vector<std::vector<Sym>> crow;
     for (int l : P.rows) {
@@ -548,7 +554,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
                 row = "(" + btid + " % " + std::to_string(BN) + ")";
                 col = "(((" + btid + " / " + std::to_string(BN) + ") + " + std::to_string(r * (BTH / BN)) + ") * 8)";
             }
-            const std::string boff = bkn ? row + " * " + std::to_string(stride) + " + " + col : koff(row, col, stride);
+            const std::string boff = bkn ? row + " * " + std::to_string(stride) + " + " + (bswz ? "(" + col + " ^ (((" + row + " >> 3) & 1) * 64))" : col) : koff(row, col, stride);
             if (grouped) {
                 // q as exact bf16 integers; this row's group s and z for the lanes' fold (the
                 // same rendering as emit_loads', whose loaded words these expressions read)
@@ -601,7 +607,8 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
                 // rows ks·32 + lq·8 + (0..3 | 4..7), column wn + j·16 + l16: in each 16-lane
                 // group, source lane s reads 4 columns 4·(s%4) of row base + s/4; lane i gets 4
                 // rows of column i
-                const std::string br = "[(" + kss + " * 32 + lq * 8 + (l16 >> 2)) * " + std::to_string(BNS) + " + wn + j * 16 + (l16 & 3) * 4]";
+                const std::string br = "[(" + kss + " * 32 + lq * 8 + (l16 >> 2)) * " + std::to_string(BNS) + " + " +
+                                       (bswz ? std::string("((wn + j * 16 + (l16 & 3) * 4) ^ ((lq & 1) * 64))") : std::string("wn + j * 16 + (l16 & 3) * 4")) + "]";
                 auto tr = [&](const std::string& arr, const std::string& dst) {
                     c2.line("  {");
                     c2.line("    const unsigned short* bp = &" + arr + "[" + buf + "]" + br + ";");
