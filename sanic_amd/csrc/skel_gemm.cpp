@@ -10,7 +10,8 @@
 //
 // Kernel shape: workgroup tile BM × BN (8 waves in 4 × 2 for 128-row tiles at least 64 columns
 // wide, else 4 waves in 2 × 2; each wave a block of 16×16 MFMA tiles), K in 64-wide steps, A and B tiles double-buffered in LDS with k contiguous so every
-// MFMA operand is one ds_read_b128; the weight leaf is loaded by the vector renderer (128-bit
+// MFMA operand is one ds_read_b128 (A planes written by a first launch skip LDS: stored in MFMA
+// fragment order, each wave loads its A fragments directly); the weight leaf is loaded by the vector renderer (128-bit
 // runs of 8 along k, per-group scale/zero once per run, packed nibbles decoded in registers);
 // project, epilogue and the narrowing store per output element.
 #include <algorithm>
@@ -309,6 +310,23 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     // launch into bf16 hi/lo planes [M][K] (plus the row slots), instead of by every one of the
     // N/BN column workgroups
     const bool pre = splitA && N / BN >= 4 && K % 512 == 0;
+    const int64_t NKT = K / 64;
+    int DEPTH = grouped ? (gvar == 2 ? 2 : 4) : 2;
+    if (!grouped && st.sched.variant == 1) DEPTH = 4;
+    if (NKT % DEPTH || NKT < 2 * DEPTH) DEPTH = 2;
+    const bool deep = NKT % DEPTH == 0 && NKT >= 2 * DEPTH;
+    // With the x·g planes written by the first launch, each wave loads its own A fragments
+    // instead of staging A through LDS: the A tile's LDS stores and fragment reads were over half
+    // of a K step's LDS traffic (B2: ≈96 of ≈176 KB per CU). The planes are then stored in
+    // fragment order — per 16-row × 32-k block, lane (l16 = row, lq = k run) at 16·lane bytes —
+    // so every fragment load is 1 KB contiguous; the two waves that share rows read the same
+    // lines (the second from L1)
+    const bool adirect = pre && deep && !getenv("SANIC_HIP_GEMM_ALDS");
+    // element offset of (row, k) in a plane: row-major, or fragment order (k a multiple of 8)
+    auto plane_off = [&](const std::string& row, const std::string& k8) {
+        if (!adirect) return "(" + row + ") * " + std::to_string(K) + " + " + k8;
+        return "((" + row + ") / 16 * " + std::to_string(K / 32) + " + (" + k8 + ") / 32) * 512 + ((" + row + ") % 16 + 16 * (((" + k8 + ") % 32) / 8)) * 8";
+    };
     int64_t hi_off = 0, lo_off = 0, rs_off = 0;
     Code kp;
     kp.indent = 1;
@@ -357,8 +375,8 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             kp.line("unsigned h_[4], l_[4];");
             for (int q = 0; q < 4; q++)
                 kp.line("split_bf16(" + av[2 * q] + ", " + av[2 * q + 1] + ", h_[" + std::to_string(q) + "], l_[" + std::to_string(q) + "]);");
-            kp.line("*(sanic_u32x4*)(ahi + mp * " + std::to_string(K) + " + " + k0 + ") = (sanic_u32x4){h_[0], h_[1], h_[2], h_[3]};");
-            kp.line("*(sanic_u32x4*)(alo + mp * " + std::to_string(K) + " + " + k0 + ") = (sanic_u32x4){l_[0], l_[1], l_[2], l_[3]};");
+            kp.line("*(sanic_u32x4*)(ahi + " + plane_off("mp", k0) + ") = (sanic_u32x4){h_[0], h_[1], h_[2], h_[3]};");
+            kp.line("*(sanic_u32x4*)(alo + " + plane_off("mp", k0) + ") = (sanic_u32x4){l_[0], l_[1], l_[2], l_[3]};");
             kp.indent--;
             kp.line("}");
         }
@@ -404,7 +422,16 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     auto emit_loads = [&](Code& c2, const std::string& kt0, const std::string& sfx) {
         // A runs
         c2.line("const idx_t mm" + sfx + " = m0 + tid / " + std::to_string(TPR) + ";");
-        for (int r = 0; r < RUNS_A && pre; r++) {
+        for (int i = 0; i < MT && adirect; i++)
+            for (int ks = 0; ks < 2; ks++) {
+                // the operand fragment itself: lane (l16, lq) holds row wm + 16·i + l16, k run lq·8
+                // of the tile's 32-deep half ks (16 contiguous bytes of the row)
+                const std::string nm = std::to_string(i) + "_" + std::to_string(ks) + sfx;
+                const std::string at = "((m0 + wm + " + std::to_string(i * 16) + ") / 16 * " + std::to_string(K / 32) + " + (" + kt0 + " + " + std::to_string(ks * 32) + ") / 32) * 512 + lane * 8";
+                c2.line("const sanic_u32x4 pah" + nm + " = *(const sanic_u32x4*)((const unsigned short*)((const char*)a.scratch + " + std::to_string(hi_off) + ") + " + at + ");");
+                c2.line("const sanic_u32x4 pal" + nm + " = *(const sanic_u32x4*)((const unsigned short*)((const char*)a.scratch + " + std::to_string(lo_off) + ") + " + at + ");");
+            }
+        for (int r = 0; r < RUNS_A && pre && !adirect; r++) {
             std::string k0 = "(" + kt0 + " + (tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8) + ")";
             const std::string rs = std::to_string(r);
             c2.line("const sanic_u32x4 pah" + rs + sfx + " = *(const sanic_u32x4*)((const unsigned short*)((const char*)a.scratch + " + std::to_string(hi_off) + ") + mm" + sfx +
@@ -495,7 +522,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         c2.line("{");
         c2.indent++;
         c2.line("const int ar = tid / " + std::to_string(TPR) + ";");
-        for (int r = 0; r < RUNS_A && pre; r++) {
+        for (int r = 0; r < RUNS_A && pre && !adirect; r++) {
             const std::string rs = std::to_string(r);
             const std::string aoff = koff("ar", "(tid % " + std::to_string(TPR) + ") * " + std::to_string(64 / TPR) + " + " + std::to_string(r * 8), AS);
             c2.line("*(sanic_u32x4*)(&a_lds[" + buf + "][" + aoff + "]) = pah" + rs + sfx + ";");
@@ -587,7 +614,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     // half's MFMAs (scheduling groups), then the second half's MFMAs — so LDS reads proceed
     // under MFMAs within each wave as well as across the two waves of a SIMD (8-wave tiles:
     // 44.5 → 41.7 µs for B2's GEMM against reading everything first)
-    auto emit_mfma = [&](Code& c2, const std::string& buf) {
+    auto emit_mfma = [&](Code& c2, const std::string& buf, const std::string& aset = "") {
         const std::string MTs = std::to_string(MT), NTs = std::to_string(NT);
         c2.line("{");
         c2.line("bf16x8 af[2][" + MTs + "], bf[2][" + NTs + "];");
@@ -596,11 +623,19 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         auto reads = [&](int ks) {
             const std::string kss = std::to_string(ks);
             const std::string aidx = "[" + koff("wm + i * 16 + l16", kss + " * 32 + lq * 8", AS) + "]";
+            if (adirect) {
+                for (int i = 0; i < MT; i++) {
+                    const std::string nm = std::to_string(i) + "_" + kss + aset;
+                    c2.line("af[" + kss + "][" + std::to_string(i) + "] = __builtin_bit_cast(bf16x8, pah" + nm + ");");
+                    c2.line("afl[" + kss + "][" + std::to_string(i) + "] = __builtin_bit_cast(bf16x8, pal" + nm + ");");
+                }
+            } else {
             c2.line("#pragma unroll");
             c2.line("for (int i = 0; i < " + MTs + "; ++i) {");
             c2.line("  af[" + kss + "][i] = *(const bf16x8*)(&a_lds[" + buf + "]" + aidx + ");");
             if (splitA) c2.line("  afl[" + kss + "][i] = *(const bf16x8*)(&a_lo[" + buf + "]" + aidx + ");");
             c2.line("}");
+            }
             c2.line("#pragma unroll");
             c2.line("for (int j = 0; j < " + NTs + "; ++j) {");
             if (bkn) {
@@ -652,7 +687,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             }
         };
         // instruction counts of one half: LDS reads and MFMAs
-        const int nds = MT * (splitA ? 2 : 1) + NT * (bkn ? 2 : 1) * (splitB ? 2 : 1);
+        const int nds = (adirect ? 0 : MT * (splitA ? 2 : 1)) + NT * (bkn ? 2 : 1) * (splitB ? 2 : 1);
         const int nmf = MT * NT * (1 + (splitA ? 1 : 0) + (splitB ? 1 : 0)) + (grouped ? MT : 0);
         reads(0);
         c2.line("__builtin_amdgcn_sched_barrier(0);");
@@ -682,14 +717,6 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         }
         c2.line("}");
     };
-    const int64_t NKT = K / 64;
-    k.line("{");
-    k.indent++;
-    emit_loads(k, "(idx_t)0", "_0");
-    emit_stores(k, "0", "_0");
-    k.indent--;
-    k.line("}");
-    k.line("__syncthreads();");
     // Loads run DEPTH tiles ahead of the MFMAs: one workgroup per CU leaves a single wave per
     // SIMD, so a tile's global loads (≈1–2 µs under load) must be in flight for several tiles'
     // MFMAs, not one. DEPTH register sets rotate in a loop unrolled by DEPTH; a set's loaded
@@ -698,10 +725,15 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     // LDS) takes tile t + DEPTH, and the set of tile t + 1 goes to LDS behind the MFMAs.
     // Depth 2 for bf16 tiles; 4 for grouped 4-bit tiles, whose per-tile MFMA work is small
     // against the load latency. Variant 1 takes the other depth.
-    int DEPTH = grouped ? (gvar == 2 ? 2 : 4) : 2;
-    if (!grouped && st.sched.variant == 1) DEPTH = 4;
-    if (NKT % DEPTH || NKT < 2 * DEPTH) DEPTH = 2;
-    const bool deep = NKT % DEPTH == 0 && NKT >= 2 * DEPTH;
+    if (!adirect) {
+        k.line("{");
+        k.indent++;
+        emit_loads(k, "(idx_t)0", "_0");
+        emit_stores(k, "0", "_0");
+        k.indent--;
+        k.line("}");
+        k.line("__syncthreads();");
+    }
     if (deep) {
         auto persistent = [&](const std::string& sfx, Code& decl) {
             Code tmp;
@@ -748,14 +780,22 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         auto set_sfx = [](int u) { return "_s" + std::to_string(u); };
         for (int u = 0; u < DEPTH; u++) names[u] = persistent(set_sfx(u), decl);
         k.s << decl.str();
+        if (adirect) {
+            // tile 0's set: its A fragments stay in registers for the first step, its B goes to LDS
+            load_into("(idx_t)0", set_sfx(0), names[0]);
+            emit_stores(k, "0", set_sfx(0));
+            k.line("__syncthreads();");
+        }
         for (int u = 1; u < DEPTH; u++) load_into("(idx_t)" + std::to_string(64 * u), set_sfx(u), names[u]);   // tiles 1..DEPTH-1
         const std::string N2 = std::to_string(NKT), DS = std::to_string(DEPTH);
         k.line("for (idx_t kt = 0; kt < " + N2 + "; kt += " + DS + ") {");
         k.indent++;
         for (int u = 0; u < DEPTH; u++) {
             // step kt+u: tile kt+u is in LDS buffer u % 2; its set takes tile kt+u+DEPTH
-            load_into("(((kt + " + std::to_string(u + DEPTH) + ") % " + N2 + ") * 64)", set_sfx(u), names[u]);
-            emit_mfma(k, std::to_string(u % 2));
+            // (A fragments in the set: the MFMAs take them before the set is reloaded)
+            if (!adirect) load_into("(((kt + " + std::to_string(u + DEPTH) + ") % " + N2 + ") * 64)", set_sfx(u), names[u]);
+            emit_mfma(k, std::to_string(u % 2), set_sfx(u));
+            if (adirect) load_into("(((kt + " + std::to_string(u + DEPTH) + ") % " + N2 + ") * 64)", set_sfx(u), names[u]);
             const int nx = (u + 1) % DEPTH;
             if (u == DEPTH - 1) {
                 k.line("if (kt + " + DS + " < " + N2 + ") {");
@@ -854,7 +894,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     if (pre) src << "extern \"C\" __global__ void __launch_bounds__(256) " << kname << "_pre(Args a) {\n" << R.entry() << kp.str() << "}\n";
     src << "extern \"C\" __global__ void __launch_bounds__(" << NTH << ") " << kname << "(Args a) {\n" << R.entry() << k.str() << "}\n";
     out.kernel_kind = "skeleton:gemm[" + std::to_string(BM) + "x" + std::to_string(BN) + (splitA ? ",a2" : "") + (splitB ? ",b2" : "") +
-                      (grouped ? ",grp" : "") + (bkn ? ",kn" : "") + (pre ? ",pre" : "") + (deep ? ",d" + std::to_string(DEPTH) : "") + ",w" + std::to_string(NTH / 64) + "]";
+                      (grouped ? ",grp" : "") + (bkn ? ",kn" : "") + (pre ? ",pre" : "") + (deep ? ",d" + std::to_string(DEPTH) : "") + ",w" + std::to_string(NTH / 64) + (adirect ? ",ad" : "") + "]";
     out.variants = grouped ? 3 : 2;
     // dequantized-weight tiles (int4): the ILP-maximising machine scheduler, D2 25.1 → 22.9 µs;
     // bf16 tiles keep the default strategy (no measurable difference)
