@@ -328,6 +328,9 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         return "((" + row + ") / 16 * " + std::to_string(K / 32) + " + (" + k8 + ") / 32) * 512 + ((" + row + ") % 16 + 16 * (((" + k8 + ") % 32) / 8)) * 8";
     };
     int64_t hi_off = 0, lo_off = 0, rs_off = 0;
+    // K slices of the first launch in fragment order (8 at K = 2048: 256 workgroups for M = 512)
+    int PKS = 1;
+    while (adirect && PKS < 8 && K % (PKS * 2 * 4 * 32) == 0 && K / (PKS * 2) >= 256) PKS *= 2;
     Code kp;
     kp.indent = 1;
     if (pre) {
@@ -336,15 +339,25 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
         lo_off = scratch;
         scratch += ((M * K * 2 + 255) / 256) * 256;
         rs_off = scratch;
-        scratch += ((M * std::max(SR, 1) * 4 + 255) / 256) * 256;
+        scratch += ((PKS * M * std::max(SR, 1) * 4 + 255) / 256) * 256;
         kp.line("const int t = threadIdx.x, lane = t & 63, wv = t >> 6;");
-        kp.line("const idx_t mp = (idx_t)blockIdx.x * 4 + wv;");
+        if (adirect) {
+            // fragment order: a workgroup takes one 16-row block and one of PKS K slices, each
+            // wave a quarter of it in 32-k blocks; lane (l16, lq) builds row l16's run lq of a
+            // block and stores it at 16·lane bytes, so every wave store is 1 KB contiguous
+            kp.line("const idx_t mp = (idx_t)(blockIdx.x / " + std::to_string(PKS) + ") * 16 + (lane & 15);");
+            kp.line("const int pks = blockIdx.x % " + std::to_string(PKS) + ";");
+        } else {
+            kp.line("const idx_t mp = (idx_t)blockIdx.x * 4 + wv;");
+        }
         kp.line("unsigned short* ahi = (unsigned short*)((char*)a.scratch + " + std::to_string(hi_off) + ");");
         kp.line("unsigned short* alo = (unsigned short*)((char*)a.scratch + " + std::to_string(lo_off) + ");");
         for (int i = 0; i < SR; i++) kp.line("float rp" + std::to_string(i) + " = 0.0f;");
-        for (int64_t i = 0; i < K / 512; i++) {
+        const int64_t PIT = adirect ? K / PKS / 4 / 32 : K / 512;   // runs per lane
+        for (int64_t i = 0; i < PIT; i++) {
             const std::string is = std::to_string(i);
-            const std::string k0 = "(" + std::to_string(i * 512) + " + lane * 8)";
+            const std::string k0 = adirect ? "(pks * " + std::to_string(K / PKS) + " + wv * " + std::to_string(K / PKS / 4) + " + " + std::to_string(i * 32) + " + (lane >> 4) * 8)"
+                                           : "(" + std::to_string(i * 512) + " + lane * 8)";
             kp.line("{");
             kp.indent++;
             R.memo.emplace_back();
@@ -380,7 +393,22 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
             kp.indent--;
             kp.line("}");
         }
-        for (int i = 0; i < SR; i++) {
+        if (adirect && SR) {
+            // row slots: the four lanes of a row, then the four waves; one partial per K slice
+            kp.line("__shared__ float rps[4][16][" + std::to_string(SR) + "];");
+            for (int i = 0; i < SR; i++) {
+                std::string r = "rp" + std::to_string(i);
+                kp.line(r + " = sanic_rows_sum(" + r + ");");
+                kp.line("if (lane < 16) rps[wv][lane][" + std::to_string(i) + "] = " + r + ";");
+            }
+            kp.line("__syncthreads();");
+            kp.line("if (t < " + std::to_string(16 * SR) + ") {");
+            kp.line("  const int r = t / " + std::to_string(SR) + ", sl = t % " + std::to_string(SR) + ";");
+            kp.line("  ((float*)((char*)a.scratch + " + std::to_string(rs_off) + "))[((idx_t)pks * " + std::to_string(M) + " + (blockIdx.x / " + std::to_string(PKS) +
+                    ") * 16 + r) * " + std::to_string(SR) + " + sl] = ((rps[0][r][sl] + rps[1][r][sl]) + rps[2][r][sl]) + rps[3][r][sl];");
+            kp.line("}");
+        }
+        for (int i = 0; i < SR && !adirect; i++) {
             std::string r = "rp" + std::to_string(i);
             kp.line(r + " = sanic_wave_sum(" + r + ");");
             kp.line("if (lane == 0) ((float*)((char*)a.scratch + " + std::to_string(rs_off) + "))[mp * " + std::to_string(SR) + " + " + std::to_string(i) + "] = " + r + ";");
@@ -829,8 +857,12 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     }
     // row slots: sum the TPR partial rows, publish per row
     if (SR && pre) {
-        k.line("for (int i = tid; i < " + std::to_string(BM * SR) + "; i += " + std::to_string(NTH) + ") rs_lds[i] = ((const float*)((const char*)a.scratch + " + std::to_string(rs_off) +
-               "))[m0 * " + std::to_string(SR) + " + i];");
+        std::string sum;
+        for (int q = 0; q < PKS; q++) {
+            const std::string pq = "((const float*)((const char*)a.scratch + " + std::to_string(rs_off) + "))[" + std::to_string((int64_t)q * M * SR) + " + m0 * " + std::to_string(SR) + " + i]";
+            sum = q ? "(" + sum + " + " + pq + ")" : pq;
+        }
+        k.line("for (int i = tid; i < " + std::to_string(BM * SR) + "; i += " + std::to_string(NTH) + ") rs_lds[i] = " + sum + ";");
         k.line("__syncthreads();");
     }
     if (SR && !pre) {
@@ -902,7 +934,7 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     std::vector<Arg> args = R.arg_list();
     if (pre) {
         args.push_back({Arg::SCRATCH, 0});
-        out.launches.push_back({kname + "_pre", "", dim3((unsigned)(M / 4)), dim3(256), 0, args});
+        out.launches.push_back({kname + "_pre", "", dim3((unsigned)(adirect ? M / 16 * PKS : M / 4)), dim3(256), 0, args});
     }
     out.launches.push_back({kname, "", dim3((unsigned)((M / BM) * (N / BN))), dim3(NTH), 0, args});
     return true;
