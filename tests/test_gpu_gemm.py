@@ -44,6 +44,33 @@ def test_rmsnorm_gemm(dev, M, K, N, kmajor, variant):
     assert err < 2e-2
 
 
+@pytest.mark.parametrize("M,K,N,kmajor", [(512, 2048, 8192, True), (64, 512, 512, False), (128, 1536, 2048, True)])
+def test_rmsnorm_gemm_fragment_order_a(dev, M, K, N, kmajor, monkeypatch):
+    """The first launch's x·g planes in MFMA fragment order (each wave loading its A fragments
+    directly, 8 × 1 waves) against the row-major planes staged through LDS
+    (SANIC_HIP_GEMM_ALDS): both within the bf16 bound of the oracle, and within one output
+    rounding of each other (the row slots are summed per K slice in the first form)."""
+    x = _bf16_vals(311, M * K).reshape(M, K)
+    g = _bf16_vals(312, K, 1.0, 0.02)
+    wbits = oracle.synth_bf16(313, N * K, "normal", 0.0, 0.02)
+    wkn = wbits.reshape(K, N) if kmajor else np.ascontiguousarray(wbits.reshape(N, K).T)
+    w = from_bf16_bits(wbits).astype(np.float64).reshape((K, N) if kmajor else (N, K))
+    want = oracle.rmsnorm_proj(x, g, np.ascontiguousarray(wkn), 1e-5)
+    outs = {}
+    for form in ("fragment", "lds"):
+        if form == "lds":
+            monkeypatch.setenv("SANIC_HIP_GEMM_ALDS", "1")
+        prog = configs.rmsnorm_projection(M=M, K=K, N=N, kmajor=kmajor)
+        got, exe = run_on_gpu(dev, prog, {"x": x, "g": g, "W": w})
+        kind = exe.stage_kernel(0)
+        assert kind.startswith("skeleton:gemm") and ",pre" in kind, kind
+        assert (",ad" in kind) == (form == "fragment"), kind
+        assert bf16_rel(got["y"], want) < 2e-2
+        outs[form] = np.asarray(got["y"], np.float64).reshape(want.shape)
+    a, b = outs["fragment"], outs["lds"]
+    assert np.max(np.abs(a - b) / np.maximum(np.abs(b), 1e-3)) <= 2.0 ** -7
+
+
 @pytest.mark.parametrize("M,K,N,G,zk,variant", [
     (128, 2048, 8192, 64, "8s", 0),      # config D2: grouped tiles (q on the MFMA, s/z folded per tile)
     (128, 2048, 8192, 64, "8s", 1),      # the other load depth
