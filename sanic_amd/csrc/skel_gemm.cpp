@@ -309,8 +309,8 @@ bool lower_gemm(const sanic_program_desc* d, int si, int64_t& scratch, LoweredSt
     // instead of staging A through LDS: the A tile's LDS stores and fragment reads were over half
     // of a K step's LDS traffic (B2: ≈96 of ≈176 KB per CU). The planes are then stored in
     // fragment order — per 16-row × 32-k block, lane (l16 = row, lq = k run) at 16·lane bytes —
-    // so every fragment load is 1 KB contiguous; the two waves that share rows read the same
-    // lines (the second from L1)
+    // so every fragment load is 1 KB contiguous (in 4-wave tiles, where two waves share rows,
+    // both load them; the second from L1)
     const bool adirect = pre && deep && !getenv("SANIC_HIP_GEMM_ALDS");
     // element offset of (row, k) in a plane: row-major, or fragment order (k a multiple of 8)
     auto plane_off = [&](const std::string& row, const std::string& k8) {
